@@ -1,0 +1,107 @@
+/*
+ * mi355_fa.h — C ABI of the MI355X (gfx950) masked FlashAttention forward.
+ *
+ * One operator: O = softmax(Q·Kᵀ·(1/√d) + mask)·V over [B,H,S,d] tensors, where
+ * the additive mask (0 = visible, -inf = blocked, finite = bias) is broadcast
+ * over heads and K/V may carry fewer heads than Q (GQA, kv_head = h / (H/Hk)).
+ *
+ * Plain pointers and sizes only; no torch types cross this boundary. The
+ * library never allocates device memory: split-KV partials live in a
+ * caller-provided workspace whose size `mi355_fa_workspace_bytes` reports.
+ * All work is enqueued on the caller's stream; nothing synchronises.
+ *
+ * Reference interfaces these entry points replace (Defyli/custom_ops):
+ *   - mi355_fa_params        ↔ FA_mask_params           csrc/fa/common/fa_fwd_params.h:18-71
+ *   - mi355_fa_fwd           ↔ mha_fwd_with_mask_cuda   csrc/fa/fa_fwd_op.cu:46-197
+ *                              (validation :53-108, launch :191-194) and
+ *                              fa_fwd_launch            csrc/fa/fa_fwd_launch.h:573-603
+ *   - mi355_fa_num_splits    ↔ fa_mask_sm89_num_splits  csrc/fa/fa_fwd_launch.h:137-170
+ *   - mi355_fa_workspace_bytes ↔ the oaccum/lseaccum torch::empty allocations
+ *                              csrc/fa/fa_fwd_launch.h:289-297
+ */
+#ifndef MI355_FA_H
+#define MI355_FA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355_FA_ABI_VERSION 1
+
+/* Error codes returned by the entry points (0 = success). */
+enum {
+  MI355_FA_OK = 0,
+  MI355_FA_EINVAL = 1,     /* argument/contract violation (message filled)       */
+  MI355_FA_EWORKSPACE = 2, /* workspace missing or too small for the split plan   */
+  MI355_FA_ELAUNCH = 3,    /* HIP launch error (message carries hipGetErrorString) */
+  MI355_FA_EDEVICE = 4     /* current device is not gfx950                        */
+};
+
+/* Element type of q/k/v/mask/out (all five share it). */
+enum { MI355_FA_FP16 = 0, MI355_FA_BF16 = 1 };
+
+/*
+ * Launch parameters. Strides are in ELEMENTS. Layouts:
+ *   q    [B, H,  Sq, d]   o [B, H, Sq, d]
+ *   k, v [B, Hk, Sk, d]   innermost (d) stride must be 1
+ *   mask [B, 1, mask_seqlen_q >= Sq, mask_seqlen_k >= Sk], innermost stride 1
+ * Mask columns >= seqlen_k are always treated as blocked whatever they hold;
+ * mask rows >= seqlen_q are never read for output. Sk need not be a multiple
+ * of 8: the kernel predicates the K/V tail and reads unaligned mask rows
+ * element-wise, so no padded copy is ever made.
+ */
+typedef struct mi355_fa_params {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* mask;
+  void* o;
+
+  int64_t q_batch_stride, q_head_stride, q_row_stride;
+  int64_t k_batch_stride, k_head_stride, k_row_stride;
+  int64_t v_batch_stride, v_head_stride, v_row_stride;
+  int64_t o_batch_stride, o_head_stride, o_row_stride;
+  int64_t mask_batch_stride, mask_row_stride;
+
+  int32_t b, h, h_k;
+  int32_t seqlen_q, seqlen_k;
+  int32_t mask_seqlen_q, mask_seqlen_k;
+  int32_t d;          /* 64 or 128 */
+  int32_t dtype;      /* MI355_FA_FP16 | MI355_FA_BF16 */
+  float scale_softmax; /* 1/sqrt(d) in the reference op; any positive value allowed */
+
+  /* Split-KV: 0 = let the cost model choose; >= 1 forces that many splits. */
+  int32_t num_splits;
+  /* Device workspace for split-KV partials (may be NULL when no split is planned). */
+  void* workspace;
+  size_t workspace_bytes;
+} mi355_fa_params;
+
+/* Run the forward pass on `stream` (a hipStream_t; NULL = legacy default stream).
+ * Returns 0 on success; otherwise writes a NUL-terminated message into err. */
+int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errlen);
+
+/* Number of KV splits the launcher will use for these params (after the cost
+ * model, the MI355_FA_NUM_SPLITS override and clamping). */
+int mi355_fa_num_splits(const mi355_fa_params* p);
+
+/* Bytes of workspace mi355_fa_fwd needs for these params (0 when unsplit). */
+size_t mi355_fa_workspace_bytes(const mi355_fa_params* p);
+
+/* Pure cost model, exposed for host tests: splits for a problem of
+ * total_mblocks row-tiles, num_n_blocks key-tiles, on num_cus compute units. */
+int mi355_fa_cost_model_splits(int total_mblocks, int num_n_blocks, int block_m,
+                               int head_dim, int num_cus);
+
+/* ABI version (MI355_FA_ABI_VERSION) and a build string. */
+int mi355_fa_abi_version(void);
+const char* mi355_fa_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355_FA_H */
