@@ -58,10 +58,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 128;      // query rows per workgroup
 constexpr int kBN = 64;       // keys per KV tile
-constexpr int kWaves = 4;     // wave64s per workgroup
-constexpr int kThreads = kWaves * 64;
 constexpr int kMaxSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -86,6 +83,32 @@ __device__ __forceinline__ To bitcast(const From& x) {
   return __builtin_bit_cast(To, x);
 }
 
+// ── buffer resources ──────────────────────────────────────────────────────────
+// Raw buffer loads/stores with 32-bit offsets: the hardware returns 0 for reads
+// (and drops writes) at offsets >= num_records. Each resource is bounded to the
+// valid rows of one head / one batch, so K/V rows >= Sk, Q/O rows >= Sq and mask
+// rows >= mask_seqlen_q need no predicate. All variable offsets are passed as the
+// per-lane (VGPR) offset, which is what the range check covers.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcFlags);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+}
+// 16 bytes per lane from the buffer straight into LDS: lane i of the wave lands
+// at lds + 16·i (gfx950 LDS DMA), no VGPR staging.
+__device__ __forceinline__ void bload16_lds(rsrc_t r, uint16_t* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void wait_vmem() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), other counters untouched
+}
+
 // ── kernel parameters (device copy, passed by value) ──────────────────────────
 struct KParams {
   const uint16_t* q;
@@ -94,23 +117,24 @@ struct KParams {
   const uint16_t* mask;
   uint16_t* o;
   float* o_part;   // [splits][B*H][Sq][D] fp32 (split path)
-  float* lse_part; // [splits][B*H][Sq]    fp32, log2 domain
+  float* lse_part; // [splits][B*H][Sq]    fp32, natural log
 
-  int64_t q_bs, q_hs, q_rs;
-  int64_t k_bs, k_hs, k_rs;
-  int64_t v_bs, v_hs, v_rs;
-  int64_t o_bs, o_hs, o_rs;
-  int64_t m_bs, m_rs;
+  int64_t q_bs, q_hs;
+  int64_t k_bs, k_hs;
+  int64_t v_bs, v_hs;
+  int64_t o_bs, o_hs;
+  int64_t m_bs;
+  int q_rs, k_rs, v_rs, o_rs, m_rs;  // row strides (elements)
 
   int b, h, ratio;   // ratio = H / Hk
   int sq, sk;
-  int num_m;         // ceil(Sq / kBM)
+  int msq;           // mask rows present
+  int num_m;         // ceil(Sq / BM)
   int num_n;         // ceil(Sk / kBN)
   int num_splits;
   int n_per_split;   // tiles per split
   int total;         // grid size (workgroups)
-  int mask_vec;      // 1: mask rows 16-byte aligned → vector loads
-  float scale_log2;  // scale * log2(e)
+  float scale;       // softmax scale (1/sqrt(d) in the reference op)
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -122,126 +146,138 @@ __device__ __forceinline__ int xcd_remap(int L, int total) {
   return (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
 
-// ── LDS layout ────────────────────────────────────────────────────────────────
-//  sK  [kBN][D + 8]      K rows, 16-byte pad per row (bank spread for b128 reads)
-//  sVt [D][kBN + 8]      Vᵀ; inside every 16-key group the key order is
-//                        {0-3, 8-11, 4-7, 12-15} so lane-group g reads 8 keys at +8g
-//  sM  [kBM][kBN + 8]    mask; inside every 32-key block lane-group g's 16 keys
-//                        {g*4 + (i/4)*8 + i%4} are stored contiguously at +16g
-template <int D> struct Smem {
-  static constexpr int kKStride = D + 8;
-  static constexpr int kVStride = kBN + 8;
-  static constexpr int kMStride = kBN + 8;
-  static constexpr int kKElems = kBN * kKStride;
-  static constexpr int kVElems = D * kVStride;
-  static constexpr int kMElems = kBM * kMStride;
-  static constexpr int kBytes = 2 * (kKElems + kVElems + kMElems);
+// ── tile geometry and LDS layout ──────────────────────────────────────────────
+// Sᵀ = K·Qᵀ is computed with K rows permuted: LDS row r of a 32-key block holds
+// key π(r) = ((r/4)%2)·16 + (r/8)·4 + r%4, so in the 32x32 C layout the lane
+// (query q, half g) owns the 16 CONSECUTIVE keys g·16 .. g·16+15 of the block.
+// Mask reads, tail predicates and the PV operand order all follow from that.
+//
+//  sK[2]   [kBN rows][D]   16-byte units, unit c of row r at slot c ^ (r % UPR)
+//  sM[2]   [BM rows][kBN]  unit u of row m at slot u ^ ((m/2) % 8)
+//  sVt[2]  [D][kBN + 8]    Vᵀ in natural key order, 16-byte row pad
+template <int D, int WAVES> struct Geo {
+  static constexpr int kBM = 32 * WAVES;
+  static constexpr int kThreads = 64 * WAVES;
+  static constexpr int kUPR = D / 8;                 // 16-byte units per K row
+  static constexpr int kKBytes = kBN * D * 2;
+  static constexpr int kMBytes = kBM * kBN * 2;
+  static constexpr int kVStride = kBN + 8;           // elements
+  static constexpr int kVBytes = D * kVStride * 2;
+  static constexpr int kKOff = 0;
+  static constexpr int kMOff = 2 * kKBytes;
+  static constexpr int kVOff = kMOff + 2 * kMBytes;
+  static constexpr int kBytes = kVOff + 2 * kVBytes;
+  static constexpr int kKWaveLoads = kBN * kUPR / 64 / WAVES;   // LDS-DMA instrs per wave
+  static constexpr int kMWaveLoads = kBM * 8 / 64 / WAVES;
+  static constexpr int kVItems = 16 * (D / 8);                  // (key quad, d chunk)
 };
 
-// Registers holding one KV tile in flight (global → regs → LDS).
-template <int D> struct TileRegs {
-  static constexpr int kKChunks = kBN * D / 8 / kThreads;   // 16-byte chunks per thread
-  static constexpr int kVItems = 16 * (D / 8);              // (key quad, d chunk) items
-  static constexpr int kMChunks = kBM * kBN / 8 / kThreads;
-  u32x4 k[kKChunks];
-  u32x4 v[4];
-  u32x4 m[kMChunks];
+__device__ __forceinline__ int key_perm(int r) {   // π within a 32-key block
+  return ((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3);
+}
+__device__ __forceinline__ int mask_swz(int m) { return (m >> 1) & 7; }
+
+template <int D, int WAVES, bool MDIRECT>
+struct Stage {
+  typedef Geo<D, WAVES> G;
+  // per-lane source offsets for this lane's share of the tile, tile position excluded
+  uint32_t k_off[G::kKWaveLoads];
+  uint32_t m_off[G::kMWaveLoads];
+  uint32_t v_off;
+  u32x4 vreg[4];
+  u32x4 mreg[MDIRECT ? 1 : G::kMWaveLoads];
+
+  __device__ __forceinline__ void init(const KParams& p, int wave, int lane, int tid, int m0) {
+#pragma unroll
+    for (int i = 0; i < G::kKWaveLoads; ++i) {
+      const int u = (i * WAVES + wave) * 64 + lane;      // LDS unit written by this lane
+      const int r = u / G::kUPR, slot = u % G::kUPR;
+      const int c = slot ^ (r % G::kUPR);
+      const int key = (r & ~31) + key_perm(r & 31);
+      k_off[i] = (uint32_t)(key * p.k_rs + c * 8) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < G::kMWaveLoads; ++i) {
+      const int u = (i * WAVES + wave) * 64 + lane;
+      const int m = u / 8, slot = u % 8;
+      const int c = slot ^ mask_swz(m);
+      m_off[i] = (uint32_t)((m0 + m) * p.m_rs + c * 8) * 2u;
+    }
+    v_off = (uint32_t)((4 * (tid % 16)) * p.v_rs + (tid / 16) * 8) * 2u;
+  }
+
+  // Issue tile n: K (and the mask when rows are 16-byte aligned) by LDS DMA into
+  // buffer `buf`, V (and an unaligned mask) into registers.
+  __device__ __forceinline__ void issue(const KParams& p, int n, int wave, int tid, uint8_t* smem,
+                                        int buf, rsrc_t rk, rsrc_t rv, rsrc_t rm) {
+    const uint32_t key0 = (uint32_t)n * kBN;
+    uint16_t* sK = (uint16_t*)(smem + G::kKOff + buf * G::kKBytes);
+    uint16_t* sM = (uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
+    const uint32_t kshift = key0 * (uint32_t)p.k_rs * 2u;
+#pragma unroll
+    for (int i = 0; i < G::kKWaveLoads; ++i)
+      bload16_lds(rk, sK + (i * WAVES + wave) * 64 * 8, k_off[i] + kshift);
+    if constexpr (MDIRECT) {
+#pragma unroll
+      for (int i = 0; i < G::kMWaveLoads; ++i)
+        bload16_lds(rm, sM + (i * WAVES + wave) * 64 * 8, m_off[i] + key0 * 2u);
+    } else {
+      const int lane = tid & 63;
+#pragma unroll
+      for (int i = 0; i < G::kMWaveLoads; ++i) {
+        const int u = (i * WAVES + wave) * 64 + lane;
+        const int c = (u % 8) ^ mask_swz(u / 8);
+        const int kc = (int)key0 + c * 8;
+        const uint32_t off = m_off[i] + key0 * 2u;
+        if (kc + 8 <= p.sk) {
+          mreg[i] = bload16(rm, off);
+        } else {   // chunk reaching past Sk: element loads, never straddling the buffer end
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = (kc + 2 * j < p.sk)
+                ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j, 0, 0) : 0u;
+            const uint32_t hi = (kc + 2 * j + 1 < p.sk)
+                ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j + 2, 0, 0) : 0u;
+            w[j] = (lo & 0xffffu) | (hi << 16);
+          }
+          mreg[i] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+      }
+    }
+    if (tid < G::kVItems) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        vreg[kk] = bload16(rv, v_off + (key0 + kk) * (uint32_t)p.v_rs * 2u);
+    }
+  }
+
+  // Registers → LDS: Vᵀ (4 keys × 8 d transposed with v_perm) and a staged mask.
+  __device__ __forceinline__ void commit(int wave, int tid, uint8_t* smem, int buf) {
+    uint16_t* sVt = (uint16_t*)(smem + G::kVOff + buf * G::kVBytes);
+    if (tid < G::kVItems) {
+      const int a = tid % 16, c = tid / 16;
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) {
+        const int w = dd / 2;
+        const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
+        u32x2 out;
+        out[0] = __builtin_amdgcn_perm(vreg[1][w], vreg[0][w], sel);
+        out[1] = __builtin_amdgcn_perm(vreg[3][w], vreg[2][w], sel);
+        *reinterpret_cast<u32x2*>(sVt + (c * 8 + dd) * G::kVStride + 4 * a) = out;
+      }
+    }
+    if constexpr (!MDIRECT) {
+      uint16_t* sM = (uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
+      const int lane = tid & 63;
+#pragma unroll
+      for (int i = 0; i < G::kMWaveLoads; ++i) {
+        const int u = (i * WAVES + wave) * 64 + lane;
+        *reinterpret_cast<u32x4*>(sM + u * 8) = mreg[i];
+      }
+    }
+  }
 };
-
-template <int D>
-__device__ __forceinline__ void load_tile(const KParams& p, TileRegs<D>& r, int tid, int n,
-                                          const uint16_t* kbase, const uint16_t* vbase,
-                                          const uint16_t* mbase, int m0) {
-  const int key0 = n * kBN;
-  // K: row-major chunks, 16 bytes each.
-  constexpr int kCPR = D / 8;  // chunks per row
-#pragma unroll
-  for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
-    const int ci = tid + i * kThreads;
-    const int row = ci / kCPR, c = ci % kCPR;
-    const int key = key0 + row;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (key < p.sk) val = *reinterpret_cast<const u32x4*>(kbase + (int64_t)key * p.k_rs + c * 8);
-    r.k[i] = val;
-  }
-  // V: thread owns 4 consecutive keys × 8 d-values, transposed at store time.
-  if (tid < TileRegs<D>::kVItems) {
-    const int a = tid % 16, c = tid / 16;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int key = key0 + 4 * a + kk;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (key < p.sk) val = *reinterpret_cast<const u32x4*>(vbase + (int64_t)key * p.v_rs + c * 8);
-      r.v[kk] = val;
-    }
-  }
-  // Mask: 8 consecutive keys of one row per chunk.
-#pragma unroll
-  for (int i = 0; i < TileRegs<D>::kMChunks; ++i) {
-    const int ci = tid + i * kThreads;
-    const int row = ci / 8, qd = ci % 8;
-    const int m = m0 + row;
-    const int key = key0 + qd * 8;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (m < p.sq) {
-      const uint16_t* src = mbase + (int64_t)m * p.m_rs + key;
-      if (p.mask_vec && key + 8 <= p.sk) {
-        val = *reinterpret_cast<const u32x4*>(src);
-      } else {
-        uint16_t e[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) e[j] = (key + j < p.sk) ? src[j] : (uint16_t)0;
-        val[0] = e[0] | ((uint32_t)e[1] << 16);
-        val[1] = e[2] | ((uint32_t)e[3] << 16);
-        val[2] = e[4] | ((uint32_t)e[5] << 16);
-        val[3] = e[6] | ((uint32_t)e[7] << 16);
-      }
-    }
-    r.m[i] = val;
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D>& r, int tid, uint16_t* sK,
-                                           uint16_t* sVt, uint16_t* sM) {
-  typedef Smem<D> S;
-  constexpr int kCPR = D / 8;
-#pragma unroll
-  for (int i = 0; i < TileRegs<D>::kKChunks; ++i) {
-    const int ci = tid + i * kThreads;
-    const int row = ci / kCPR, c = ci % kCPR;
-    *reinterpret_cast<u32x4*>(sK + row * S::kKStride + c * 8) = r.k[i];
-  }
-  if (tid < TileRegs<D>::kVItems) {
-    const int a = tid % 16, c = tid / 16;
-    // position of key 4a inside the permuted 16-key group
-    const int pos = (a / 4) * 16 + (a % 2) * 8 + ((a / 2) % 2) * 4;
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const int w = dd / 2;
-      const bool hi = dd & 1;
-      uint32_t x0 = r.v[0][w], x1 = r.v[1][w], x2 = r.v[2][w], x3 = r.v[3][w];
-      u32x2 out;
-      if (hi) {
-        out[0] = (x0 >> 16) | (x1 & 0xffff0000u);
-        out[1] = (x2 >> 16) | (x3 & 0xffff0000u);
-      } else {
-        out[0] = (x0 & 0xffffu) | (x1 << 16);
-        out[1] = (x2 & 0xffffu) | (x3 << 16);
-      }
-      *reinterpret_cast<u32x2*>(sVt + (c * 8 + dd) * S::kVStride + pos) = out;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < TileRegs<D>::kMChunks; ++i) {
-    const int ci = tid + i * kThreads;
-    const int row = ci / 8, qd = ci % 8;
-    const int kb = qd / 4, ib = (qd % 4) * 4;
-    uint16_t* dst = sM + row * S::kMStride + kb * 32 + ib;
-    *reinterpret_cast<u32x2*>(dst) = u32x2{r.m[i][0], r.m[i][1]};       // keys 8qd+0..3 → g=0
-    *reinterpret_cast<u32x2*>(dst + 16) = u32x2{r.m[i][2], r.m[i][3]};  // keys 8qd+4..7 → g=1
-  }
-}
 
 template <bool BF16>
 __device__ __forceinline__ f32x16 mask_to_f32(u32x4 lo, u32x4 hi) {
@@ -254,17 +290,31 @@ __device__ __forceinline__ f32x16 mask_to_f32(u32x4 lo, u32x4 hi) {
   return r;
 }
 
-template <int D, bool BF16, bool SPLIT>
-__global__ __launch_bounds__(kThreads, 2) void fa_fwd_kernel(const KParams p) {
+// max / sum with the lane 32 apart (the other half of the same query row)
+__device__ __forceinline__ float xhalf_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Lazy rescaling: the running max used for the exponent only moves when a new
+// score exceeds it by more than kRescaleSlack (natural-log units, = 8 in log2),
+// so P stays <= 2^8 and the O/l rescale is skipped on almost every tile. The
+// result is the same softmax: O and l are always scaled by the same factor.
+constexpr float kRescaleSlack = 5.5451774f;   // 8·ln 2
+
+template <int D, bool BF16, bool SPLIT, int WAVES, bool MDIRECT>
+__global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   typedef typename Elt<BF16>::v8 V8;
-  typedef Smem<D> S;
+  typedef Geo<D, WAVES> G;
   constexpr int KD = D / 16;  // MFMA k-steps over the head dim
   constexpr int DB = D / 32;  // 32-wide d blocks of the output
+  constexpr int kBM = G::kBM;
 
-  extern __shared__ __align__(16) uint16_t smem[];
-  uint16_t* sK = smem;
-  uint16_t* sVt = sK + S::kKElems;
-  uint16_t* sM = sVt + S::kVElems;
+  extern __shared__ __align__(16) uint8_t smem[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -284,35 +334,44 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_kernel(const KParams p) {
   const int n_begin = split * p.n_per_split;
   const int n_end = min(n_begin + p.n_per_split, p.num_n);
 
-  const uint16_t* qbase = p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs;
-  const uint16_t* kbase = p.k + (int64_t)b * p.k_bs + (int64_t)hk * p.k_hs;
-  const uint16_t* vbase = p.v + (int64_t)b * p.v_bs + (int64_t)hk * p.v_hs;
-  const uint16_t* mbase = p.mask + (int64_t)b * p.m_bs;
+  const rsrc_t rq = make_rsrc(p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs,
+                              (uint32_t)p.sq * p.q_rs * 2u);
+  const rsrc_t rk = make_rsrc(p.k + (int64_t)b * p.k_bs + (int64_t)hk * p.k_hs,
+                              (uint32_t)p.sk * p.k_rs * 2u);
+  const rsrc_t rv = make_rsrc(p.v + (int64_t)b * p.v_bs + (int64_t)hk * p.v_hs,
+                              (uint32_t)p.sk * p.v_rs * 2u);
+  const rsrc_t rm = make_rsrc(p.mask + (int64_t)b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+
+  Stage<D, WAVES, MDIRECT> st;
+  st.init(p, wave, lane, tid, m0);
+  if (n_begin < n_end) st.issue(p, n_begin, wave, tid, smem, 0, rk, rv, rm);
 
   // Q for this lane's row, as the B operand of Sᵀ = K·Qᵀ (kept for the whole loop).
   const int qrow = m0 + wave * 32 + l32;
   V8 qreg[KD];
 #pragma unroll
-  for (int kd = 0; kd < KD; ++kd) {
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (qrow < p.sq) val = *reinterpret_cast<const u32x4*>(qbase + (int64_t)qrow * p.q_rs + kd * 16 + g * 8);
-    qreg[kd] = bitcast<V8>(val);
-  }
+  for (int kd = 0; kd < KD; ++kd)
+    qreg[kd] = bitcast<V8>(bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u));
 
   f32x16 oacc[DB];
 #pragma unroll
   for (int i = 0; i < DB; ++i) oacc[i] = f32x16{};
-  float m_run = -INFINITY;
-  float l_run = 0.f;
+  float m_run = -INFINITY;   // running max (natural-log domain), lazily updated
+  float mlog2 = 0.f;         // m_run·log2(e), 0 while the row has seen nothing
+  float l_run = 0.f;         // this lane's partial row sum (its 16 keys of each block)
 
-  TileRegs<D> regs;
-  if (n_begin < n_end) load_tile<D>(p, regs, tid, n_begin, kbase, vbase, mbase, m0);
+  if (n_begin < n_end) st.commit(wave, tid, smem, 0);
 
   for (int n = n_begin; n < n_end; ++n) {
-    __syncthreads();
-    store_tile<D>(regs, tid, sK, sVt, sM);
-    __syncthreads();
-    if (n + 1 < n_end) load_tile<D>(p, regs, tid, n + 1, kbase, vbase, mbase, m0);
+    const int buf = (n - n_begin) & 1;
+    wait_vmem();        // this lane's LDS-DMA for tile n has landed
+    __syncthreads();    // ... and everyone's; tile n-1 is no longer being read
+    const bool more = n + 1 < n_end;
+    if (more) st.issue(p, n + 1, wave, tid, smem, buf ^ 1, rk, rv, rm);
+
+    const uint16_t* sK = (const uint16_t*)(smem + G::kKOff + buf * G::kKBytes);
+    const uint16_t* sM = (const uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
+    const uint16_t* sVt = (const uint16_t*)(smem + G::kVOff + buf * G::kVBytes);
 
     // ── Sᵀ = K·Qᵀ : two 32-key blocks ─────────────────────────────────────
     f32x16 s[2] = {f32x16{}, f32x16{}};
@@ -320,77 +379,93 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_kernel(const KParams p) {
     for (int kd = 0; kd < KD; ++kd) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
+        const int r = kb * 32 + l32;
+        const int c = 2 * kd + g;
         const V8 a = bitcast<V8>(*reinterpret_cast<const u32x4*>(
-            sK + (kb * 32 + l32) * S::kKStride + kd * 16 + g * 8));
+            sK + (r * G::kUPR + (c ^ (r % G::kUPR))) * 8));
         s[kb] = Elt<BF16>::mfma(a, qreg[kd], s[kb]);
       }
     }
 
-    // ── mask add (log2 domain), tail predicate, online softmax ───────────
-    const uint16_t* mrow = sM + (wave * 32 + l32) * S::kMStride + g * 16;
-    const bool tail = (n + 1) * kBN > p.sk;
+    // ── x = S·scale + mask (natural-log domain); tail keys forced to -inf ──
+    const int mr = wave * 32 + l32;
+    const uint16_t* mrow = sM + mr * kBN;
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(mrow + kb * 32);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(mrow + kb * 32 + 8);
+      const int u0 = 4 * kb + 2 * g;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(mrow + ((u0 ^ mask_swz(mr)) * 8));
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(mrow + (((u0 + 1) ^ mask_swz(mr)) * 8));
       const f32x16 mk = mask_to_f32<BF16>(lo, hi);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = s[kb][i] * p.scale_log2 + mk[i] * kLog2e;
-        if (tail) {
-          const int key = n * kBN + kb * 32 + (i / 4) * 8 + g * 4 + (i % 4);
-          x = (key < p.sk) ? x : -INFINITY;
-        }
-        s[kb][i] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int i = 0; i < 16; ++i) s[kb][i] = __builtin_fmaf(s[kb][i], p.scale, mk[i]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
+    if ((n + 1) * kBN > p.sk) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = n * kBN + kb * 32 + g * 16 + i;
+          s[kb][i] = (key < p.sk) ? s[kb][i] : -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    mx = xhalf_max(mx);
 
-    float lsum = 0.f;
+    // ── lazy online-softmax rescale (wave-uniform branch) ─────────────────
+    const bool need = mx > m_run + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      // lanes that keep their max scale by exactly 1 (also avoids -inf - -inf)
+      const float m_new = need ? mx : m_run;
+      const float alpha = need ? __builtin_amdgcn_exp2f((m_run - mx) * kLog2e) : 1.f;  // -inf → 0
+      m_run = m_new;
+      mlog2 = (m_new == -INFINITY) ? 0.f : m_new * kLog2e;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+    }
+
+    // ── P = exp(x − m), rounded to the input dtype as the PV B operand ────
     V8 pb[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       f32x8 p0, p1;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float e0 = __builtin_amdgcn_exp2f(s[kb][i] - m_use);
-        const float e1 = __builtin_amdgcn_exp2f(s[kb][8 + i] - m_use);
-        lsum += e0 + e1;
-        p0[i] = e0;
-        p1[i] = e1;
+        p0[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], kLog2e, -mlog2));
+        p1[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][8 + i], kLog2e, -mlog2));
       }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l_run += p0[i] + p1[i];
       pb[kb * 2 + 0] = __builtin_convertvector(p0, V8);
       pb[kb * 2 + 1] = __builtin_convertvector(p1, V8);
     }
-    l_run = l_run * alpha + lsum;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
 
-    // ── Oᵀ += Vᵀ·Pᵀ ─────────────────────────────────────────────────────
+    // ── Oᵀ += Vᵀ·Pᵀ : K-step j covers keys 32(j/2) + 16g + 8(j%2) + [0,8) ──
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const V8 a = bitcast<V8>(*reinterpret_cast<const u32x4*>(
-            sVt + (db * 32 + l32) * S::kVStride + j * 16 + g * 8));
+            sVt + (db * 32 + l32) * G::kVStride + (j / 2) * 32 + g * 16 + (j % 2) * 8));
         oacc[db] = Elt<BF16>::mfma(a, pb[j], oacc[db]);
       }
     }
+
+    if (more) st.commit(wave, tid, smem, buf ^ 1);
   }
 
   // ── epilogue ────────────────────────────────────────────────────────────
-  const float l = l_run + __shfl_xor(l_run, 32);
+  const float l = xhalf_sum(l_run);
   const float inv = (l == 0.f || l != l) ? 1.f : 1.f / l;
-  if (qrow >= p.sq) return;
 
   if constexpr (!SPLIT) {
-    uint16_t* orow = p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs + (int64_t)qrow * p.o_rs;
+    const rsrc_t ro = make_rsrc(p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs,
+                                (uint32_t)p.sq * p.o_rs * 2u);
+    const uint32_t obase = (uint32_t)(qrow * p.o_rs + g * 4) * 2u;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -403,10 +478,11 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_kernel(const KParams p) {
         u32x2 packed;
         if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
         else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
-        *reinterpret_cast<u32x2*>(orow + db * 32 + q4 * 8 + g * 4) = packed;
+        __builtin_amdgcn_raw_buffer_store_b64(packed, ro, obase + (db * 32 + q4 * 8) * 2u, 0, 0);
       }
     }
   } else {
+    if (qrow >= p.sq) return;
     const int64_t bh = (int64_t)b * p.h + h;
     const int64_t slab = (int64_t)p.b * p.h * p.sq;   // rows per split
     const int64_t prow = (int64_t)split * slab + bh * p.sq + qrow;
@@ -422,7 +498,9 @@ __global__ __launch_bounds__(kThreads, 2) void fa_fwd_kernel(const KParams p) {
       }
     }
     if (g == 0) {
-      p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY : m_run + __builtin_amdgcn_logf(l);
+      // natural-log LSE of this split's row (reference convention lse = m + log l)
+      p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY
+                                               : m_run + __builtin_amdgcn_logf(l) * 0.69314718f;
     }
   }
 }
@@ -437,32 +515,54 @@ struct CParams {
   int64_t rows;  // B*H*Sq
 };
 
-// One thread = 4 consecutive d-values of one row. Weights w_s = 2^(lse_s - max) / Σ.
+// Workgroup = kRows rows × D columns; thread = 4 consecutive d-values of a row.
+// Phase 1 stages the rows' LSEs in LDS and turns them into weights
+// w_s = exp(lse_s − max) / Σ (all-(-inf) row → all weights 0 → output 0);
+// phase 2 accumulates Σ w_s·O_s with independent, unrolled loads.
 template <int D, bool BF16>
 __global__ __launch_bounds__(256) void fa_combine_kernel(const CParams p) {
   constexpr int kTPR = D / 4;              // threads per row
   constexpr int kRows = 256 / kTPR;        // rows per workgroup
+  __shared__ float sw[kMaxSplits * kRows];
   const int tid = threadIdx.x;
-  const int64_t row = (int64_t)blockIdx.x * kRows + tid / kTPR;
-  const int c4 = tid % kTPR;
-  if (row >= p.rows) return;
+  const int64_t row0 = (int64_t)blockIdx.x * kRows;
   const int64_t slab = p.rows;
-  float mx = -INFINITY;
-  for (int s = 0; s < p.num_splits; ++s) mx = fmaxf(mx, p.lse_part[s * slab + row]);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float wsum = 0.f;
-  if (mx != -INFINITY) {
-    for (int s = 0; s < p.num_splits; ++s) {
-      const float w = __builtin_amdgcn_exp2f(p.lse_part[s * slab + row] - mx);
-      if (w > 0.f) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(p.o_part + (s * slab + row) * D + c4 * 4);
-        acc += w * v;
-        wsum += w;
-      }
-    }
+  const int S = p.num_splits;
+  for (int i = tid; i < S * kRows; i += 256) {
+    const int s = i / kRows, r = i % kRows;
+    const int64_t row = row0 + r;
+    sw[i] = (row < p.rows) ? p.lse_part[s * slab + row] : -INFINITY;
   }
-  const float inv = (wsum > 0.f) ? 1.f / wsum : 0.f;
-  acc *= inv;
+  __syncthreads();
+  if (tid < kRows) {
+    float mx = -INFINITY;
+    for (int s = 0; s < S; ++s) mx = fmaxf(mx, sw[s * kRows + tid]);
+    const float mxc = (mx == -INFINITY) ? 0.f : mx;
+    float sum = 0.f;
+    for (int s = 0; s < S; ++s) {
+      const float w = __builtin_amdgcn_exp2f((sw[s * kRows + tid] - mxc) * kLog2e);
+      sw[s * kRows + tid] = w;
+      sum += w;
+    }
+    const float inv = (sum > 0.f) ? 1.f / sum : 0.f;
+    for (int s = 0; s < S; ++s) sw[s * kRows + tid] *= inv;
+  }
+  __syncthreads();
+  const int r = tid / kTPR;
+  const int c4 = tid % kTPR;
+  const int64_t row = row0 + r;
+  if (row >= p.rows) return;
+  const float* src = p.o_part + row * D + c4 * 4;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = 0;
+  for (; s + 4 <= S; s += 4) {
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + (s + u) * slab * D);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += sw[(s + u) * kRows + r] * v[u];
+  }
+  for (; s < S; ++s) acc += sw[s * kRows + r] * *reinterpret_cast<const f32x4*>(src + s * slab * D);
   const int64_t bh = row / p.sq;
   const int m = (int)(row % p.sq);
   const int b = (int)(bh / p.h), h = (int)(bh % p.h);
@@ -551,24 +651,36 @@ static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int 
 }
 
 struct Plan {
-  int num_m, num_n, splits, n_per_split;
+  int waves, block_m, num_m, num_n, splits, n_per_split;
   size_t o_part_bytes, lse_bytes, ws_bytes;
 };
 
+// Tile plan: 8 waves × 32 rows (BM = 256) when that grid fills the chip,
+// otherwise BM = 128 (4 waves), and split-KV when even that under-fills it.
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
-  pl.num_m = ceil_div(p->seqlen_q, kBM);
   pl.num_n = ceil_div(p->seqlen_k, kBN);
+  const int bh = p->b * p->h;
   int s = p->num_splits;
   if (s <= 0) {
     const char* env = getenv("MI355_FA_NUM_SPLITS");
     if (env && atoi(env) > 0) s = atoi(env);
   }
-  if (s <= 0) s = cost_model_splits(p->b * p->h * pl.num_m, pl.num_n, kBM, p->d, cus);
+  const int m256 = ceil_div(p->seqlen_q, 256), m128 = ceil_div(p->seqlen_q, 128);
+  if (s <= 0) {
+    if ((float)bh * m256 >= 0.8f * cus) {
+      s = 1;
+    } else {
+      s = cost_model_splits(bh * m128, pl.num_n, 128, p->d, cus);
+    }
+  }
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > pl.num_n) s = pl.num_n;
   if (s < 1) s = 1;
   pl.splits = s;
+  pl.waves = (s == 1 && (float)bh * m256 >= 0.8f * cus) ? 8 : 4;
+  pl.block_m = 32 * pl.waves;
+  pl.num_m = ceil_div(p->seqlen_q, pl.block_m);
   pl.n_per_split = (s > 1) ? ceil_div(pl.num_n, s) : pl.num_n;
   if (s > 1) {
     const size_t rows = (size_t)s * p->b * p->h * p->seqlen_q;
@@ -628,20 +740,39 @@ static int validate(const mi355_fa_params* p, char* err, size_t errlen) {
   return MI355_FA_OK;
 }
 
+template <int D, bool BF16, bool SPLIT, int WAVES, bool MDIRECT>
+static hipError_t launch_main(const KParams& kp, hipStream_t st) {
+  auto kern = fa_fwd_kernel<D, BF16, SPLIT, WAVES, MDIRECT>;
+  constexpr int smem = Geo<D, WAVES>::kBytes;
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(once, [&] {
+    attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  });
+  if (attr_err != hipSuccess) return attr_err;
+  hipLaunchKernelGGL(kern, dim3(kp.total), dim3(64 * WAVES), smem, st, kp);
+  return hipGetLastError();
+}
+
 template <int D, bool BF16>
-static hipError_t launch(const KParams& kp, const CParams& cp, bool split, hipStream_t st) {
-  const size_t smem = Smem<D>::kBytes;
-  if (split) {
-    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, true>), dim3(kp.total), dim3(kThreads), smem, st, kp);
-    hipError_t e = hipGetLastError();
+static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, bool mdirect,
+                         hipStream_t st) {
+  hipError_t e;
+  if (pl.splits > 1) {
+    e = mdirect ? launch_main<D, BF16, true, 4, true>(kp, st)
+                : launch_main<D, BF16, true, 4, false>(kp, st);
     if (e != hipSuccess) return e;
     constexpr int kRows = 256 / (D / 4);
     const int64_t blocks = (cp.rows + kRows - 1) / kRows;
     hipLaunchKernelGGL((fa_combine_kernel<D, BF16>), dim3((unsigned)blocks), dim3(256), 0, st, cp);
-  } else {
-    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, false>), dim3(kp.total), dim3(kThreads), smem, st, kp);
+    return hipGetLastError();
   }
-  return hipGetLastError();
+  if (pl.waves == 8)
+    return mdirect ? launch_main<D, BF16, false, 8, true>(kp, st)
+                   : launch_main<D, BF16, false, 8, false>(kp, st);
+  return mdirect ? launch_main<D, BF16, false, 4, true>(kp, st)
+                 : launch_main<D, BF16, false, 4, false>(kp, st);
 }
 
 }  // namespace mi355fa
@@ -653,7 +784,7 @@ extern "C" {
 int mi355_fa_abi_version(void) { return MI355_FA_ABI_VERSION; }
 
 const char* mi355_fa_build_info(void) {
-  return "mi355_fa gfx950 BM=128 BN=64 waves=4 mfma32x32x16 splitkv+combine";
+  return "mi355_fa gfx950 BM=128/256 BN=64 waves=4/8 mfma32x32x16 lds-dma splitkv+combine";
 }
 
 int mi355_fa_cost_model_splits(int total_mblocks, int num_n_blocks, int block_m, int head_dim,
@@ -686,6 +817,23 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
     set_err(err, errlen, "problem too large: %lld workgroups", (long long)total);
     return MI355_FA_EINVAL;
   }
+  // Buffer offsets are 32-bit: every per-head / per-batch byte range the kernel
+  // addresses (including the rounded-up last row tile) must stay below 2^32.
+  {
+    const uint64_t rows_q = (uint64_t)pl.num_m * pl.block_m, rows_k = (uint64_t)pl.num_n * kBN;
+    const uint64_t lim = 0xffffffffull - 4096;
+    const uint64_t need[] = {
+        rows_q * (uint64_t)p->q_row_stride * 2, rows_q * (uint64_t)p->o_row_stride * 2,
+        rows_k * (uint64_t)p->k_row_stride * 2, rows_k * (uint64_t)p->v_row_stride * 2,
+        (rows_q * (uint64_t)p->mask_row_stride + rows_k) * 2,
+        (uint64_t)p->mask_seqlen_q * (uint64_t)p->mask_row_stride * 2};
+    for (uint64_t n : need) {
+      if (n > lim) {
+        set_err(err, errlen, "problem too large: a per-head or per-batch tensor slice exceeds 4 GiB");
+        return MI355_FA_EINVAL;
+      }
+    }
+  }
   const bool split = pl.splits > 1;
   if (split && (!p->workspace || p->workspace_bytes < pl.ws_bytes)) {
     set_err(err, errlen, "split-KV needs %zu workspace bytes, got %zu", pl.ws_bytes, p->workspace_bytes);
@@ -698,19 +846,17 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.v = (const uint16_t*)p->v;
   kp.mask = (const uint16_t*)p->mask;
   kp.o = (uint16_t*)p->o;
-  kp.q_bs = p->q_batch_stride; kp.q_hs = p->q_head_stride; kp.q_rs = p->q_row_stride;
-  kp.k_bs = p->k_batch_stride; kp.k_hs = p->k_head_stride; kp.k_rs = p->k_row_stride;
-  kp.v_bs = p->v_batch_stride; kp.v_hs = p->v_head_stride; kp.v_rs = p->v_row_stride;
-  kp.o_bs = p->o_batch_stride; kp.o_hs = p->o_head_stride; kp.o_rs = p->o_row_stride;
-  kp.m_bs = p->mask_batch_stride; kp.m_rs = p->mask_row_stride;
+  kp.q_bs = p->q_batch_stride; kp.q_hs = p->q_head_stride; kp.q_rs = (int)p->q_row_stride;
+  kp.k_bs = p->k_batch_stride; kp.k_hs = p->k_head_stride; kp.k_rs = (int)p->k_row_stride;
+  kp.v_bs = p->v_batch_stride; kp.v_hs = p->v_head_stride; kp.v_rs = (int)p->v_row_stride;
+  kp.o_bs = p->o_batch_stride; kp.o_hs = p->o_head_stride; kp.o_rs = (int)p->o_row_stride;
+  kp.m_bs = p->mask_batch_stride; kp.m_rs = (int)p->mask_row_stride;
   kp.b = p->b; kp.h = p->h; kp.ratio = p->h / p->h_k;
-  kp.sq = p->seqlen_q; kp.sk = p->seqlen_k;
+  kp.sq = p->seqlen_q; kp.sk = p->seqlen_k; kp.msq = p->mask_seqlen_q;
   kp.num_m = pl.num_m; kp.num_n = pl.num_n;
   kp.num_splits = pl.splits; kp.n_per_split = pl.n_per_split;
   kp.total = (int)total;
-  kp.mask_vec = (((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
-                 (p->mask_row_stride & 7) == 0) ? 1 : 0;
-  kp.scale_log2 = p->scale_softmax * kLog2e;
+  kp.scale = p->scale_softmax;
 
   CParams cp{};
   if (split) {
@@ -727,8 +873,12 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   const bool bf16 = p->dtype == MI355_FA_BF16;
-  if (p->d == 128) e = bf16 ? launch<128, true>(kp, cp, split, st) : launch<128, false>(kp, cp, split, st);
-  else e = bf16 ? launch<64, true>(kp, cp, split, st) : launch<64, false>(kp, cp, split, st);
+  const bool mdirect = ((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
+                       (p->mask_row_stride & 7) == 0;
+  if (p->d == 128)
+    e = bf16 ? launch<128, true>(kp, cp, pl, mdirect, st) : launch<128, false>(kp, cp, pl, mdirect, st);
+  else
+    e = bf16 ? launch<64, true>(kp, cp, pl, mdirect, st) : launch<64, false>(kp, cp, pl, mdirect, st);
   if (e != hipSuccess) {
     set_err(err, errlen, "mi355_fa launch failed: %s", hipGetErrorString(e));
     return MI355_FA_ELAUNCH;
