@@ -45,6 +45,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "mi355_fa.h"
 
@@ -152,77 +153,87 @@ __device__ __forceinline__ int xcd_remap(int L, int total) {
 // (query q, half g) owns the 16 CONSECUTIVE keys g·16 .. g·16+15 of the block.
 // Mask reads, tail predicates and the PV operand order all follow from that.
 //
-//  sK[2]   [kBN rows][D]   16-byte units, unit c of row r at slot c ^ (r % UPR)
-//  sM[2]   [BM rows][kBN]  unit u of row m at slot u ^ ((m/2) % 8)
-//  sVt[2]  [D][kBN + 8]    Vᵀ in natural key order, 16-byte row pad
+// Every buffer is written by LDS DMA in 1 KiB wave-chunks (lane i → +16·i), so
+// layouts are permutations of 16-byte units, chosen for conflict-free reads:
+//  sK[2]  [kBN][D]   unit c of row r at slot c ^ (r % UPR)          (ds_read_b128)
+//  sV[2]  [kBN][D]   unit c of row r at slot c ^ swzV(r)            (ds_read_b64_tr_b16)
+//  sM[2]  [BM][kBN]  unit u of row m at slot u ^ ((m/2) % 8)        (ds_read_b128)
 template <int D, int WAVES> struct Geo {
   static constexpr int kBM = 32 * WAVES;
   static constexpr int kThreads = 64 * WAVES;
-  static constexpr int kUPR = D / 8;                 // 16-byte units per K row
+  static constexpr int kUPR = D / 8;                 // 16-byte units per K/V row
   static constexpr int kKBytes = kBN * D * 2;
   static constexpr int kMBytes = kBM * kBN * 2;
-  static constexpr int kVStride = kBN + 8;           // elements
-  static constexpr int kVBytes = D * kVStride * 2;
   static constexpr int kKOff = 0;
-  static constexpr int kMOff = 2 * kKBytes;
-  static constexpr int kVOff = kMOff + 2 * kMBytes;
-  static constexpr int kBytes = kVOff + 2 * kVBytes;
-  static constexpr int kKWaveLoads = kBN * kUPR / 64 / WAVES;   // LDS-DMA instrs per wave
+  static constexpr int kVOff = 2 * kKBytes;
+  static constexpr int kMOff = kVOff + 2 * kKBytes;
+  static constexpr int kBytes = kMOff + 2 * kMBytes;
+  static constexpr int kKVWaveLoads = kBN * kUPR / 64 / WAVES;  // LDS-DMA instrs per wave
   static constexpr int kMWaveLoads = kBM * 8 / 64 / WAVES;
-  static constexpr int kVItems = 16 * (D / 8);                  // (key quad, d chunk)
 };
 
 __device__ __forceinline__ int key_perm(int r) {   // π within a 32-key block
   return ((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3);
 }
 __device__ __forceinline__ int mask_swz(int m) { return (m >> 1) & 7; }
+template <int D> __device__ __forceinline__ int v_swz(int r) {
+  return (D == 128) ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+}
 
 template <int D, int WAVES, bool MDIRECT>
 struct Stage {
   typedef Geo<D, WAVES> G;
-  // per-lane source offsets for this lane's share of the tile, tile position excluded
-  uint32_t k_off[G::kKWaveLoads];
+  // per-lane source byte offsets of this lane's share of a tile (tile position excluded)
+  uint32_t k_off[G::kKVWaveLoads];
+  uint32_t v_off[G::kKVWaveLoads];
   uint32_t m_off[G::kMWaveLoads];
-  uint32_t v_off;
-  u32x4 vreg[4];
   u32x4 mreg[MDIRECT ? 1 : G::kMWaveLoads];
 
-  __device__ __forceinline__ void init(const KParams& p, int wave, int lane, int tid, int m0) {
+  __device__ __forceinline__ void init(const KParams& p, int wave, int lane, int m0) {
 #pragma unroll
-    for (int i = 0; i < G::kKWaveLoads; ++i) {
+    for (int i = 0; i < G::kKVWaveLoads; ++i) {
       const int u = (i * WAVES + wave) * 64 + lane;      // LDS unit written by this lane
       const int r = u / G::kUPR, slot = u % G::kUPR;
-      const int c = slot ^ (r % G::kUPR);
       const int key = (r & ~31) + key_perm(r & 31);
-      k_off[i] = (uint32_t)(key * p.k_rs + c * 8) * 2u;
+      k_off[i] = (uint32_t)(key * p.k_rs + (slot ^ (r % G::kUPR)) * 8) * 2u;
+      v_off[i] = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
     }
 #pragma unroll
     for (int i = 0; i < G::kMWaveLoads; ++i) {
       const int u = (i * WAVES + wave) * 64 + lane;
       const int m = u / 8, slot = u % 8;
-      const int c = slot ^ mask_swz(m);
-      m_off[i] = (uint32_t)((m0 + m) * p.m_rs + c * 8) * 2u;
+      m_off[i] = (uint32_t)((m0 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
     }
-    v_off = (uint32_t)((4 * (tid % 16)) * p.v_rs + (tid / 16) * 8) * 2u;
   }
 
-  // Issue tile n: K (and the mask when rows are 16-byte aligned) by LDS DMA into
-  // buffer `buf`, V (and an unaligned mask) into registers.
-  __device__ __forceinline__ void issue(const KParams& p, int n, int wave, int tid, uint8_t* smem,
-                                        int buf, rsrc_t rk, rsrc_t rv, rsrc_t rm) {
-    const uint32_t key0 = (uint32_t)n * kBN;
+  __device__ __forceinline__ void issue_k(const KParams& p, int n, int wave, uint8_t* smem, int buf,
+                                          rsrc_t rk) {
     uint16_t* sK = (uint16_t*)(smem + G::kKOff + buf * G::kKBytes);
-    uint16_t* sM = (uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
-    const uint32_t kshift = key0 * (uint32_t)p.k_rs * 2u;
+    const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.k_rs * 2u;
 #pragma unroll
-    for (int i = 0; i < G::kKWaveLoads; ++i)
-      bload16_lds(rk, sK + (i * WAVES + wave) * 64 * 8, k_off[i] + kshift);
+    for (int i = 0; i < G::kKVWaveLoads; ++i)
+      bload16_lds(rk, sK + (i * WAVES + wave) * 64 * 8, k_off[i] + sh);
+  }
+
+  __device__ __forceinline__ void issue_v(const KParams& p, int n, int wave, uint8_t* smem, int buf,
+                                          rsrc_t rv) {
+    uint16_t* sV = (uint16_t*)(smem + G::kVOff + buf * G::kKBytes);
+    const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.v_rs * 2u;
+#pragma unroll
+    for (int i = 0; i < G::kKVWaveLoads; ++i)
+      bload16_lds(rv, sV + (i * WAVES + wave) * 64 * 8, v_off[i] + sh);
+  }
+
+  // Mask tile n: LDS DMA when rows are 16-byte aligned, else registers (commit_m).
+  __device__ __forceinline__ void issue_m(const KParams& p, int n, int wave, int lane, uint8_t* smem,
+                                          int buf, rsrc_t rm) {
+    const uint32_t key0 = (uint32_t)n * kBN;
     if constexpr (MDIRECT) {
+      uint16_t* sM = (uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
 #pragma unroll
       for (int i = 0; i < G::kMWaveLoads; ++i)
         bload16_lds(rm, sM + (i * WAVES + wave) * 64 * 8, m_off[i] + key0 * 2u);
     } else {
-      const int lane = tid & 63;
 #pragma unroll
       for (int i = 0; i < G::kMWaveLoads; ++i) {
         const int u = (i * WAVES + wave) * 64 + lane;
@@ -245,31 +256,11 @@ struct Stage {
         }
       }
     }
-    if (tid < G::kVItems) {
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        vreg[kk] = bload16(rv, v_off + (key0 + kk) * (uint32_t)p.v_rs * 2u);
-    }
   }
 
-  // Registers → LDS: Vᵀ (4 keys × 8 d transposed with v_perm) and a staged mask.
-  __device__ __forceinline__ void commit(int wave, int tid, uint8_t* smem, int buf) {
-    uint16_t* sVt = (uint16_t*)(smem + G::kVOff + buf * G::kVBytes);
-    if (tid < G::kVItems) {
-      const int a = tid % 16, c = tid / 16;
-#pragma unroll
-      for (int dd = 0; dd < 8; ++dd) {
-        const int w = dd / 2;
-        const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-        u32x2 out;
-        out[0] = __builtin_amdgcn_perm(vreg[1][w], vreg[0][w], sel);
-        out[1] = __builtin_amdgcn_perm(vreg[3][w], vreg[2][w], sel);
-        *reinterpret_cast<u32x2*>(sVt + (c * 8 + dd) * G::kVStride + 4 * a) = out;
-      }
-    }
+  __device__ __forceinline__ void commit_m(int wave, int lane, uint8_t* smem, int buf) {
     if constexpr (!MDIRECT) {
       uint16_t* sM = (uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
-      const int lane = tid & 63;
 #pragma unroll
       for (int i = 0; i < G::kMWaveLoads; ++i) {
         const int u = (i * WAVES + wave) * 64 + lane;
@@ -300,27 +291,163 @@ __device__ __forceinline__ float xhalf_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Σ of the 8 rounded P values of one MFMA operand, two per dot2 (fp32 accumulate).
+template <bool BF16>
+__device__ __forceinline__ float psum8(typename Elt<BF16>::v8 v, float acc) {
+  if constexpr (BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[2 * i], v[2 * i + 1]}, one, acc, false);
+  } else {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc = __builtin_amdgcn_fdot2(f16x2{v[2 * i], v[2 * i + 1]}, one, acc, false);
+  }
+  return acc;
+}
+
 // Lazy rescaling: the running max used for the exponent only moves when a new
 // score exceeds it by more than kRescaleSlack (natural-log units, = 8 in log2),
 // so P stays <= 2^8 and the O/l rescale is skipped on almost every tile. The
 // result is the same softmax: O and l are always scaled by the same factor.
 constexpr float kRescaleSlack = 5.5451774f;   // 8·ln 2
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
 template <int D, bool BF16, bool SPLIT, int WAVES, bool MDIRECT>
-__global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
+struct Attn {
   typedef typename Elt<BF16>::v8 V8;
   typedef Geo<D, WAVES> G;
-  constexpr int KD = D / 16;  // MFMA k-steps over the head dim
-  constexpr int DB = D / 32;  // 32-wide d blocks of the output
+  static constexpr int KD = D / 16;  // MFMA k-steps over the head dim
+  static constexpr int DB = D / 32;  // 32-wide d blocks of the output
+
+  const KParams& p;
+  uint8_t* smem;
+  int tid, lane, wave, l32, g;
+  int n_begin, n_end;
+  rsrc_t rk, rv, rm;
+  Stage<D, WAVES, MDIRECT> st;
+  V8 qreg[KD];
+  f32x16 oacc[DB];
+  f32x16 s[2];          // Sᵀ of the tile being softmaxed
+  float m_run, mlog2, l_run;
+  uint32_t k_rd[KD];    // per-lane LDS byte offsets of the K operand reads (buffer 0)
+  uint32_t v_rd[DB];    // per-lane LDS byte offsets of the Vᵀ transpose reads, per d block
+  uint32_t m_rd[4];     // per-lane LDS byte offsets of the mask reads (buffer 0)
+
+  __device__ __forceinline__ Attn(const KParams& p_, uint8_t* smem_) : p(p_), smem(smem_) {}
+
+  // Sᵀ (two 32-key blocks) for the tile in K buffer KB.
+  template <int KB>
+  __device__ __forceinline__ void qk(f32x16 (&acc)[2]) {
+    acc[0] = f32x16{};
+    acc[1] = f32x16{};
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const V8 a = bitcast<V8>(*reinterpret_cast<const u32x4*>(
+            smem + G::kKOff + KB * G::kKBytes + kb * 32 * D * 2 + k_rd[kd]));
+        acc[kb] = Elt<BF16>::mfma(a, qreg[kd], acc[kb]);
+      }
+    }
+  }
+
+  // Softmax of tile n (mask buffer MB) fused with O += Vᵀ·Pᵀ (V buffer MB) and,
+  // when NEXT, Sᵀ of tile n+1 from K buffer MB^1 issued in between.
+  template <int MB, bool NEXT>
+  __device__ __forceinline__ void step(int n) {
+    f32x16 s_next[2];
+    // scores → x = S·scale + mask, natural-log domain
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const uint8_t* mb = smem + G::kMOff + MB * G::kMBytes;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * kb]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * kb + 1]);
+      const f32x16 mk = mask_to_f32<BF16>(lo, hi);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[kb][i] = __builtin_fmaf(s[kb][i], p.scale, mk[i]);
+    }
+    if constexpr (NEXT) qk<MB ^ 1>(s_next);
+    if ((n + 1) * kBN > p.sk) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = n * kBN + kb * 32 + g * 16 + i;
+          s[kb][i] = (key < p.sk) ? s[kb][i] : -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    mx = xhalf_max(mx);
+
+    const bool need = mx > m_run + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      // lanes that keep their max scale by exactly 1 (also avoids -inf - -inf)
+      const float alpha = need ? __builtin_amdgcn_exp2f((m_run - mx) * kLog2e) : 1.f;  // -inf → 0
+      m_run = need ? mx : m_run;
+      mlog2 = (m_run == -INFINITY) ? 0.f : m_run * kLog2e;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+    }
+
+    // P = exp(x − m) rounded to the dtype; Oᵀ += Vᵀ·Pᵀ one 16-key step at a time
+    const uint8_t* vb = smem + G::kVOff + MB * G::kKBytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f32x8 pf;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j / 2][(j % 2) * 8 + i], kLog2e, -mlog2));
+      const V8 pb = __builtin_convertvector(pf, V8);
+      l_run = psum8<BF16>(pb, l_run);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        // rows (keys) 32(j/2) + 16g + 8(j%2) + [0,8) of Vᵀ column db·32 + l32
+        const int off = ((j / 2) * 32 + (j % 2) * 8) * D * 2;
+        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + v_rd[db] + off));
+        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vb + v_rd[db] + off + 4 * D * 2));
+        const V8 a = bitcast<V8>(__builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+        oacc[db] = Elt<BF16>::mfma(a, pb, oacc[db]);
+      }
+    }
+    if constexpr (NEXT) {
+      s[0] = s_next[0];
+      s[1] = s_next[1];
+    }
+  }
+};
+
+// PIPE = software-pipelined QKᵀ(n+1) under softmax(n); used with one wave per
+// SIMD (4 waves), where the wave has the whole 512-entry register file.
+template <int D, bool BF16, bool SPLIT, int WAVES, bool MDIRECT>
+__global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
+  constexpr bool PIPE = (WAVES == 4);
+  typedef Attn<D, BF16, SPLIT, WAVES, MDIRECT> A;
+  typedef Geo<D, WAVES> G;
+  typedef typename A::V8 V8;
   constexpr int kBM = G::kBM;
+  constexpr int DB = A::DB;
 
   extern __shared__ __align__(16) uint8_t smem[];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int l32 = lane & 31;
-  const int g = lane >> 5;
+  A a(p, smem);
+  a.tid = threadIdx.x;
+  a.lane = a.tid & 63;
+  a.wave = a.tid >> 6;
+  a.l32 = a.lane & 31;
+  a.g = a.lane >> 5;
+  const int lane = a.lane, wave = a.wave, l32 = a.l32, g = a.g;
 
   // logical tile id → (b, h, split, m_block)
   int t = xcd_remap(blockIdx.x, p.total);
@@ -331,135 +458,113 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   const int hk = h / p.ratio;
 
   const int m0 = mb * kBM;
-  const int n_begin = split * p.n_per_split;
-  const int n_end = min(n_begin + p.n_per_split, p.num_n);
+  const int nb = split * p.n_per_split;
+  const int ne = min(nb + p.n_per_split, p.num_n);
 
   const rsrc_t rq = make_rsrc(p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs,
                               (uint32_t)p.sq * p.q_rs * 2u);
-  const rsrc_t rk = make_rsrc(p.k + (int64_t)b * p.k_bs + (int64_t)hk * p.k_hs,
-                              (uint32_t)p.sk * p.k_rs * 2u);
-  const rsrc_t rv = make_rsrc(p.v + (int64_t)b * p.v_bs + (int64_t)hk * p.v_hs,
-                              (uint32_t)p.sk * p.v_rs * 2u);
-  const rsrc_t rm = make_rsrc(p.mask + (int64_t)b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+  a.rk = make_rsrc(p.k + (int64_t)b * p.k_bs + (int64_t)hk * p.k_hs, (uint32_t)p.sk * p.k_rs * 2u);
+  a.rv = make_rsrc(p.v + (int64_t)b * p.v_bs + (int64_t)hk * p.v_hs, (uint32_t)p.sk * p.v_rs * 2u);
+  a.rm = make_rsrc(p.mask + (int64_t)b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
 
-  Stage<D, WAVES, MDIRECT> st;
-  st.init(p, wave, lane, tid, m0);
-  if (n_begin < n_end) st.issue(p, n_begin, wave, tid, smem, 0, rk, rv, rm);
+  // per-lane LDS read offsets (buffer 0; other buffers are compile-time shifts)
+#pragma unroll
+  for (int kd = 0; kd < A::KD; ++kd) {
+    const int c = 2 * kd + g;
+    a.k_rd[kd] = (uint32_t)(l32 * G::kUPR + (c ^ (l32 % G::kUPR))) * 16u;
+  }
+  {
+    // ds_read_b64_tr_b16: in each 16-lane group, source lane s supplies 4 d-values
+    // of key base + s/4 and output lane o receives keys base..base+3 of column
+    // D0 + o. Source lane s therefore reads key row 16g + s/4 (+ a compile-time
+    // 32(j/2) + 8(j%2) + 4h, a multiple of 4), columns 32·db + 16(group%2) + 4(s%4).
+    const int s16 = lane & 15, grp = lane >> 4;
+    const int row = 16 * g + s16 / 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int d = 32 * db + 16 * (grp & 1) + 4 * (s16 & 3);
+      a.v_rd[db] = (uint32_t)(row * D * 2 + (((d / 8) ^ v_swz<D>(row)) * 16) + (d % 8) * 2);
+    }
+  }
+  {
+    const int mr = wave * 32 + l32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = (i / 2) * 4 + 2 * g + (i % 2);           // units of keys kb·32 + 16g + 8(i%2)
+      a.m_rd[i] = (uint32_t)(mr * kBN + ((u ^ mask_swz(mr)) * 8)) * 2u;
+    }
+  }
+
+  a.st.init(p, wave, lane, m0);
+  // Zero both V buffers once: a V row the tail's DMA leaves unwritten then holds
+  // 0 or an earlier tile's finite values, and its P is 0, so it adds nothing.
+  for (int i = a.tid; i < 2 * G::kKBytes / 16; i += G::kThreads)
+    *reinterpret_cast<u32x4*>(smem + G::kVOff + i * 16) = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
+  if (nb < ne) {
+    a.st.issue_k(p, nb, wave, smem, 0, a.rk);
+    a.st.issue_v(p, nb, wave, smem, 0, a.rv);
+    a.st.issue_m(p, nb, wave, lane, smem, 0, a.rm);
+    if (PIPE && nb + 1 < ne) a.st.issue_k(p, nb + 1, wave, smem, 1, a.rk);
+  }
 
   // Q for this lane's row, as the B operand of Sᵀ = K·Qᵀ (kept for the whole loop).
   const int qrow = m0 + wave * 32 + l32;
-  V8 qreg[KD];
 #pragma unroll
-  for (int kd = 0; kd < KD; ++kd)
-    qreg[kd] = bitcast<V8>(bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u));
+  for (int kd = 0; kd < A::KD; ++kd)
+    a.qreg[kd] = bitcast<V8>(bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u));
 
-  f32x16 oacc[DB];
 #pragma unroll
-  for (int i = 0; i < DB; ++i) oacc[i] = f32x16{};
-  float m_run = -INFINITY;   // running max (natural-log domain), lazily updated
-  float mlog2 = 0.f;         // m_run·log2(e), 0 while the row has seen nothing
-  float l_run = 0.f;         // this lane's partial row sum (its 16 keys of each block)
+  for (int i = 0; i < DB; ++i) a.oacc[i] = f32x16{};
+  a.m_run = -INFINITY;
+  a.mlog2 = 0.f;
+  a.l_run = 0.f;
 
-  if (n_begin < n_end) st.commit(wave, tid, smem, 0);
-
-  for (int n = n_begin; n < n_end; ++n) {
-    const int buf = (n - n_begin) & 1;
-    wait_vmem();        // this lane's LDS-DMA for tile n has landed
-    __syncthreads();    // ... and everyone's; tile n-1 is no longer being read
-    const bool more = n + 1 < n_end;
-    if (more) st.issue(p, n + 1, wave, tid, smem, buf ^ 1, rk, rv, rm);
-
-    const uint16_t* sK = (const uint16_t*)(smem + G::kKOff + buf * G::kKBytes);
-    const uint16_t* sM = (const uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
-    const uint16_t* sVt = (const uint16_t*)(smem + G::kVOff + buf * G::kVBytes);
-
-    // ── Sᵀ = K·Qᵀ : two 32-key blocks ─────────────────────────────────────
-    f32x16 s[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-    for (int kd = 0; kd < KD; ++kd) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int r = kb * 32 + l32;
-        const int c = 2 * kd + g;
-        const V8 a = bitcast<V8>(*reinterpret_cast<const u32x4*>(
-            sK + (r * G::kUPR + (c ^ (r % G::kUPR))) * 8));
-        s[kb] = Elt<BF16>::mfma(a, qreg[kd], s[kb]);
-      }
-    }
-
-    // ── x = S·scale + mask (natural-log domain); tail keys forced to -inf ──
-    const int mr = wave * 32 + l32;
-    const uint16_t* mrow = sM + mr * kBN;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int u0 = 4 * kb + 2 * g;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(mrow + ((u0 ^ mask_swz(mr)) * 8));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(mrow + (((u0 + 1) ^ mask_swz(mr)) * 8));
-      const f32x16 mk = mask_to_f32<BF16>(lo, hi);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[kb][i] = __builtin_fmaf(s[kb][i], p.scale, mk[i]);
-    }
-    if ((n + 1) * kBN > p.sk) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = n * kBN + kb * 32 + g * 16 + i;
-          s[kb][i] = (key < p.sk) ? s[kb][i] : -INFINITY;
-        }
-    }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-    mx = xhalf_max(mx);
-
-    // ── lazy online-softmax rescale (wave-uniform branch) ─────────────────
-    const bool need = mx > m_run + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      // lanes that keep their max scale by exactly 1 (also avoids -inf - -inf)
-      const float m_new = need ? mx : m_run;
-      const float alpha = need ? __builtin_amdgcn_exp2f((m_run - mx) * kLog2e) : 1.f;  // -inf → 0
-      m_run = m_new;
-      mlog2 = (m_new == -INFINITY) ? 0.f : m_new * kLog2e;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
-    }
-
-    // ── P = exp(x − m), rounded to the input dtype as the PV B operand ────
-    V8 pb[4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x8 p0, p1;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        p0[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], kLog2e, -mlog2));
-        p1[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][8 + i], kLog2e, -mlog2));
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) l_run += p0[i] + p1[i];
-      pb[kb * 2 + 0] = __builtin_convertvector(p0, V8);
-      pb[kb * 2 + 1] = __builtin_convertvector(p1, V8);
-    }
-
-    // ── Oᵀ += Vᵀ·Pᵀ : K-step j covers keys 32(j/2) + 16g + 8(j%2) + [0,8) ──
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const V8 a = bitcast<V8>(*reinterpret_cast<const u32x4*>(
-            sVt + (db * 32 + l32) * G::kVStride + (j / 2) * 32 + g * 16 + (j % 2) * 8));
-        oacc[db] = Elt<BF16>::mfma(a, pb[j], oacc[db]);
-      }
-    }
-
-    if (more) st.commit(wave, tid, smem, buf ^ 1);
+  if (nb < ne) a.st.commit_m(wave, lane, smem, 0);
+  if (PIPE && nb < ne) {
+    wait_vmem();
+    __syncthreads();
+    a.template qk<0>(a.s);
   }
 
+  // Iteration over tile n (parity P = (n - nb) % 2, compile-time): mask(n) and
+  // V(n) sit in buffer P; tile n+1's mask/V (and K) go to the buffers the
+  // previous iteration finished reading.
+  //  PIPE:  K(n+1) is already in K buffer P^1 and K(n+2) is prefetched into P;
+  //         Sᵀ(n+1) is computed while tile n is softmaxed.
+  //  !PIPE: K(n) is in K buffer P; K(n+1) is prefetched into P^1.
+  auto iter = [&](auto parity, int n) {
+    constexpr int P = decltype(parity)::value;
+    wait_vmem();
+    __syncthreads();
+    const bool more = n + 1 < ne;
+    if constexpr (PIPE) {
+      if (n + 2 < ne) a.st.issue_k(p, n + 2, wave, smem, P, a.rk);
+    } else {
+      if (more) a.st.issue_k(p, n + 1, wave, smem, P ^ 1, a.rk);
+    }
+    if (more) {
+      a.st.issue_v(p, n + 1, wave, smem, P ^ 1, a.rv);
+      a.st.issue_m(p, n + 1, wave, lane, smem, P ^ 1, a.rm);
+    }
+    if constexpr (PIPE) {
+      if (more) a.template step<P, true>(n);
+      else a.template step<P, false>(n);
+    } else {
+      a.template qk<P>(a.s);
+      a.template step<P, false>(n);
+    }
+    if (more) a.st.commit_m(wave, lane, smem, P ^ 1);
+  };
+  int n = nb;
+  for (; n + 1 < ne; n += 2) {
+    iter(std::integral_constant<int, 0>{}, n);
+    iter(std::integral_constant<int, 1>{}, n + 1);
+  }
+  if (n < ne) iter(std::integral_constant<int, 0>{}, n);
+
   // ── epilogue ────────────────────────────────────────────────────────────
-  const float l = xhalf_sum(l_run);
+  const float l = xhalf_sum(a.l_run);
   const float inv = (l == 0.f || l != l) ? 1.f : 1.f / l;
 
   if constexpr (!SPLIT) {
@@ -472,7 +577,7 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
       for (int q4 = 0; q4 < 4; ++q4) {
         f32x4 v4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
+        for (int i = 0; i < 4; ++i) v4[i] = a.oacc[db][q4 * 4 + i] * inv;
         typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
         typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
         u32x2 packed;
@@ -493,14 +598,14 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
       for (int q4 = 0; q4 < 4; ++q4) {
         f32x4 v4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
+        for (int i = 0; i < 4; ++i) v4[i] = a.oacc[db][q4 * 4 + i] * inv;
         *reinterpret_cast<f32x4*>(op + db * 32 + q4 * 8 + g * 4) = v4;
       }
     }
     if (g == 0) {
       // natural-log LSE of this split's row (reference convention lse = m + log l)
       p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY
-                                               : m_run + __builtin_amdgcn_logf(l) * 0.69314718f;
+                                               : a.m_run + __builtin_amdgcn_logf(l) * 0.69314718f;
     }
   }
 }
@@ -679,6 +784,10 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   if (s < 1) s = 1;
   pl.splits = s;
   pl.waves = (s == 1 && (float)bh * m256 >= 0.8f * cus) ? 8 : 4;
+  if (s == 1) {   // tuning override; split-KV always uses the 4-wave kernel
+    const char* wenv = getenv("MI355_FA_WAVES");
+    if (wenv && (atoi(wenv) == 4 || atoi(wenv) == 8)) pl.waves = atoi(wenv);
+  }
   pl.block_m = 32 * pl.waves;
   pl.num_m = ceil_div(p->seqlen_q, pl.block_m);
   pl.n_per_split = (s > 1) ? ceil_div(pl.num_n, s) : pl.num_n;
