@@ -12,7 +12,8 @@ inputs resident in HBM. Prints ONE JSON line:
                  MI355X dense bf16 MFMA peak, from HIP events on the launch stream
   configs      = per-config latency (µs) measured the reference's way (median
                  of N after warmup, >= 512 MB written between iterations to
-                 flush L2 + MALL; benchmark/benchmark_fa.py:115-132)
+                 flush L2 + MALL; benchmark/benchmark_fa.py:115-132), and
+                 "us_hot": back-to-back launches at settled clocks
   cpu_baseline = PyTorch fp32 math attention on this host's cores over a
                  time-bounded sample of (b, h) heads of the same workload.
 """
@@ -33,9 +34,11 @@ MI355X_HBM_GBPS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg2")
+    ap.add_argument("--settle-s", type=float, default=0.5,
+                    help="untimed back-to-back steps before warmup, in seconds (clock ramp)")
     ap.add_argument("--ref-iters", type=int, default=30)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -60,6 +63,22 @@ def ref_method_us(fn, warmup, iters, flush):
     return ts[len(ts) // 2] * 1e3
 
 
+def hot_us(fn, iters=100):
+    """Back-to-back launches at settled clocks (no flush): mean µs per launch."""
+    import torch
+    for _ in range(100):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e3
+
+
 def cpu_baseline(cfg, seconds):
     """PyTorch fp32 math path (the reference's CPU path) on host cores."""
     import torch
@@ -76,8 +95,8 @@ def cpu_baseline(cfg, seconds):
     torch_math_cpu(q, k, v, m, heads=heads[:1])   # warm-up
     done = 0
     t0 = time.perf_counter()
-    while done < len(heads) and time.perf_counter() - t0 < seconds:
-        torch_math_cpu(q, k, v, m, heads=[heads[done]])
+    while time.perf_counter() - t0 < seconds:   # whole (b, h) heads, cycling over the batch
+        torch_math_cpu(q, k, v, m, heads=[heads[done % len(heads)]])
         done += 1
     el = time.perf_counter() - t0
     flops = cfg.flops / len(heads) * done
@@ -95,7 +114,8 @@ def cpu_baseline(cfg, seconds):
         "unit": "TFLOPS",
         "cores": cores,
         "kind": "port",
-        "sample": f"{done}/{len(heads)} (b,h) heads of {cfg.name} in {el:.1f}s, fp32 torch math "
+        "sample": f"{done} (b,h) head passes ({done / len(heads):.1f}x the {len(heads)} heads of "
+                  f"{cfg.name}) in {el:.1f}s, fp32 torch math "
                   f"attention (scores+mask, guarded softmax, P@V) on {cpu_name}",
         "us_full_workload_extrapolated": round(el / done * len(heads) * 1e6, 1),
     }
@@ -119,6 +139,15 @@ def main():
     q, k, v, m = (t.to(dev) for t in make_inputs(cfg))
     fn = lambda: ops.mha_fwd_with_mask(q, k, v, m)  # noqa: E731
 
+    # The GPU's clocks take ~200 launches (~30 ms of back-to-back work) to reach
+    # their loaded steady state; settle them (untimed) before the W warmup steps.
+    settle_t0 = time.perf_counter()
+    settle_n = 0
+    while time.perf_counter() - settle_t0 < args.settle_s:
+        for _ in range(20):
+            fn()
+        settle_n += 20
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         fn()
     torch.cuda.synchronize()
@@ -151,6 +180,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_settle_steps": settle_n,
         "ms_per_step": round(ms_per_step, 5),
         "us_per_step": round(ms_per_step * 1e3, 2),
         "pct_of_bf16_peak": round(100 * value / MI355X_BF16_DENSE_TFLOPS, 2),
@@ -180,13 +210,19 @@ def main():
                 tq, tk, tv, tm = q, k, v, m
             else:
                 tq, tk, tv, tm = (t.to(dev) for t in make_inputs(c))
-            us = ref_method_us(lambda: ops.mha_fwd_with_mask(tq, tk, tv, tm), 5,
-                               args.ref_iters, flush)
+            fnc = lambda: ops.mha_fwd_with_mask(tq, tk, tv, tm)  # noqa: E731
+            us = ref_method_us(fnc, 5, args.ref_iters, flush)
+            us_hot = hot_us(fnc)
             tf = c.flops / (us * 1e-6) / 1e12
+            tf_hot = c.flops / (us_hot * 1e-6) / 1e12
             confs[name] = {"us": round(us, 2), "tflops": round(tf, 2),
                            "pct_bf16_peak": round(100 * tf / MI355X_BF16_DENSE_TFLOPS, 2),
                            "hbm_gbps_algorithmic": round(c.algorithmic_bytes / (us * 1e-6) / 1e9,
-                                                         1)}
+                                                         1),
+                           "us_hot": round(us_hot, 2),
+                           "pct_bf16_peak_hot": round(100 * tf_hot / MI355X_BF16_DENSE_TFLOPS, 2),
+                           "hbm_gbps_algorithmic_hot": round(
+                               c.algorithmic_bytes / (us_hot * 1e-6) / 1e9, 1)}
             del tq, tk, tv, tm
         del flush
         result["configs"] = confs

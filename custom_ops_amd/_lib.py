@@ -13,7 +13,7 @@ import threading
 
 import torch  # noqa: F401  (must precede the dlopen below, see module docstring)
 
-from .build import LIB_PATH
+from .build import lib_path
 
 FP16 = 0
 BF16 = 1
@@ -77,6 +77,7 @@ def load() -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
+        LIB_PATH = lib_path()
         if not os.path.exists(LIB_PATH):
             _load_error = (f"{LIB_PATH} is missing: build it with `python -m custom_ops_amd.build` "
                            f"(or __graft_entry__.build())")

@@ -17,6 +17,12 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libmi355_fa.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 
+
+def lib_path() -> str:
+    """Library the loader opens: the in-tree build, or MI355_FA_LIB (a tuning hook
+    for comparing builds of the same ABI)."""
+    return os.environ.get("MI355_FA_LIB") or LIB_PATH
+
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (unreliable on this pool).
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -13,24 +13,25 @@
 //   - kv_head = h / (H / Hk)                               fa_fwd_kernel.h:114
 //
 // Design (MI355X-native, not a translation of the CuTe kernels):
-//   * One workgroup = 4 wave64 = one tile of BM=128 query rows; each wave owns
-//     32 query rows. KV tiles of BN=64 keys.
+//   * One workgroup = WAVES wave64 (8 → BM = 256 query rows for grids that fill
+//     the chip, 4 → BM = 128 for small grids and split-KV); each wave owns 32
+//     query rows. KV tiles of BN = 64 keys.
 //   * The score tile is computed transposed, Sᵀ = K·Qᵀ, with
 //     v_mfma_f32_32x32x16_{bf16,f16}: A = K rows from LDS, B = Q held in VGPRs
 //     for the whole loop. In the 32x32 C layout a lane then owns ONE query row
 //     (column lane%32) and 16 keys, so row max / row sum are in-lane plus one
-//     exchange with lane^32.
+//     exchange with lane^32 (v_permlane32_swap).
 //   * Oᵀ = Vᵀ·Pᵀ: the Sᵀ accumulators, rounded to bf16/fp16, are directly the
 //     B operand of the PV MFMA (no LDS round trip for P). The A operand Vᵀ is
-//     produced by transposing V in registers while staging it into LDS, with
-//     the key order inside each 16-key group permuted so that every MFMA
-//     operand read is one ds_read_b128.
-//   * The mask tile is staged through LDS with coalesced 16-byte loads and a
-//     permuted key order that makes each lane's 16 mask values contiguous.
-//   * K/V/mask for tile n+1 are loaded into registers while tile n computes
-//     (one LDS buffer, two barriers per tile, 2 workgroups per CU).
-//   * Sk tails are predicated in-kernel (no padded copies); unaligned mask rows
-//     (mask row stride % 8 != 0) use element loads.
+//     read from row-major V in LDS with ds_read_b64_tr_b16.
+//   * K, V and the mask tile of tile n+1 go HBM → LDS by buffer_load ... lds
+//     (no VGPR staging) while tile n computes; double-buffered LDS, one barrier
+//     per tile. XOR swizzles keep every LDS read conflict-free.
+//   * Lazy rescaling: the running max moves only when a score exceeds it by
+//     more than 8 (log2 units); O and l are rescaled on those tiles only.
+//   * Sk tails are predicated in-kernel (buffer-resource bounds return 0 for
+//     K/V rows past Sk, scores of those keys are forced to -inf); unaligned mask
+//     rows (mask row stride % 8 != 0) are loaded through registers.
 //   * Linear workgroup ids are remapped so that consecutive logical tiles
 //     (the m-blocks of one head, the heads of one GQA group) land on the same
 //     XCD and share its L2.
@@ -106,9 +107,6 @@ __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff) {
 __device__ __forceinline__ void bload16_lds(rsrc_t r, uint16_t* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
 }
-__device__ __forceinline__ void wait_vmem() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0), other counters untouched
-}
 
 // ── kernel parameters (device copy, passed by value) ──────────────────────────
 struct KParams {
@@ -135,6 +133,7 @@ struct KParams {
   int num_splits;
   int n_per_split;   // tiles per split
   int total;         // grid size (workgroups)
+  int mask_direct;   // mask rows 16-byte aligned: the mask tile can go by LDS DMA
   float scale;       // softmax scale (1/sqrt(d) in the reference op)
 };
 
@@ -147,128 +146,25 @@ __device__ __forceinline__ int xcd_remap(int L, int total) {
   return (xcd < r) ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
 
-// ── tile geometry and LDS layout ──────────────────────────────────────────────
-// Sᵀ = K·Qᵀ is computed with K rows permuted: LDS row r of a 32-key block holds
-// key π(r) = ((r/4)%2)·16 + (r/8)·4 + r%4, so in the 32x32 C layout the lane
-// (query q, half g) owns the 16 CONSECUTIVE keys g·16 .. g·16+15 of the block.
-// Mask reads, tail predicates and the PV operand order all follow from that.
+// ── design ───────────────────────────────────────────────────────────────────
+// Each wave owns 32 query rows and computes Sᵀ = K·Qᵀ with 32x32x16 MFMAs, so a
+// lane holds the scores of ONE query row (its C column) and the row max / sum
+// need only the lane 32 apart. Q stays in registers for the whole key loop.
 //
-// Every buffer is written by LDS DMA in 1 KiB wave-chunks (lane i → +16·i), so
-// layouts are permutations of 16-byte units, chosen for conflict-free reads:
-//  sK[2]  [kBN][D]   unit c of row r at slot c ^ (r % UPR)          (ds_read_b128)
-//  sV[2]  [kBN][D]   unit c of row r at slot c ^ swzV(r)            (ds_read_b64_tr_b16)
-//  sM[2]  [BM][kBN]  unit u of row m at slot u ^ ((m/2) % 8)        (ds_read_b128)
-template <int D, int WAVES> struct Geo {
-  static constexpr int kBM = 32 * WAVES;
-  static constexpr int kThreads = 64 * WAVES;
-  static constexpr int kUPR = D / 8;                 // 16-byte units per K/V row
-  static constexpr int kKBytes = kBN * D * 2;
-  static constexpr int kMBytes = kBM * kBN * 2;
-  static constexpr int kKOff = 0;
-  static constexpr int kVOff = 2 * kKBytes;
-  static constexpr int kMOff = kVOff + 2 * kKBytes;
-  static constexpr int kBytes = kMOff + 2 * kMBytes;
-  static constexpr int kKVWaveLoads = kBN * kUPR / 64 / WAVES;  // LDS-DMA instrs per wave
-  static constexpr int kMWaveLoads = kBM * 8 / 64 / WAVES;
-};
-
+// K rows are permuted in LDS: row r of a 32-key block holds key
+// π(r) = ((r/4)%2)·16 + (r/8)·4 + r%4, so in the 32x32 C layout lane (query q,
+// half g) owns the 16 CONSECUTIVE keys g·16 .. g·16+15 of the block. Mask
+// reads, tail predicates and the PV operand order all follow from that: the
+// exponentials of 8 consecutive keys form one bf16x8 B operand of Oᵀ += Vᵀ·Pᵀ.
 __device__ __forceinline__ int key_perm(int r) {   // π within a 32-key block
   return ((r >> 2) & 1) * 16 + (r >> 3) * 4 + (r & 3);
 }
-__device__ __forceinline__ int mask_swz(int m) { return (m >> 1) & 7; }
-template <int D> __device__ __forceinline__ int v_swz(int r) {
-  return (D == 128) ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt[3:0] | [15:14])
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
-
-template <int D, int WAVES, bool MDIRECT>
-struct Stage {
-  typedef Geo<D, WAVES> G;
-  // per-lane source byte offsets of this lane's share of a tile (tile position excluded)
-  uint32_t k_off[G::kKVWaveLoads];
-  uint32_t v_off[G::kKVWaveLoads];
-  uint32_t m_off[G::kMWaveLoads];
-  u32x4 mreg[MDIRECT ? 1 : G::kMWaveLoads];
-
-  __device__ __forceinline__ void init(const KParams& p, int wave, int lane, int m0) {
-#pragma unroll
-    for (int i = 0; i < G::kKVWaveLoads; ++i) {
-      const int u = (i * WAVES + wave) * 64 + lane;      // LDS unit written by this lane
-      const int r = u / G::kUPR, slot = u % G::kUPR;
-      const int key = (r & ~31) + key_perm(r & 31);
-      k_off[i] = (uint32_t)(key * p.k_rs + (slot ^ (r % G::kUPR)) * 8) * 2u;
-      v_off[i] = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
-    }
-#pragma unroll
-    for (int i = 0; i < G::kMWaveLoads; ++i) {
-      const int u = (i * WAVES + wave) * 64 + lane;
-      const int m = u / 8, slot = u % 8;
-      m_off[i] = (uint32_t)((m0 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
-    }
-  }
-
-  __device__ __forceinline__ void issue_k(const KParams& p, int n, int wave, uint8_t* smem, int buf,
-                                          rsrc_t rk) {
-    uint16_t* sK = (uint16_t*)(smem + G::kKOff + buf * G::kKBytes);
-    const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.k_rs * 2u;
-#pragma unroll
-    for (int i = 0; i < G::kKVWaveLoads; ++i)
-      bload16_lds(rk, sK + (i * WAVES + wave) * 64 * 8, k_off[i] + sh);
-  }
-
-  __device__ __forceinline__ void issue_v(const KParams& p, int n, int wave, uint8_t* smem, int buf,
-                                          rsrc_t rv) {
-    uint16_t* sV = (uint16_t*)(smem + G::kVOff + buf * G::kKBytes);
-    const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.v_rs * 2u;
-#pragma unroll
-    for (int i = 0; i < G::kKVWaveLoads; ++i)
-      bload16_lds(rv, sV + (i * WAVES + wave) * 64 * 8, v_off[i] + sh);
-  }
-
-  // Mask tile n: LDS DMA when rows are 16-byte aligned, else registers (commit_m).
-  __device__ __forceinline__ void issue_m(const KParams& p, int n, int wave, int lane, uint8_t* smem,
-                                          int buf, rsrc_t rm) {
-    const uint32_t key0 = (uint32_t)n * kBN;
-    if constexpr (MDIRECT) {
-      uint16_t* sM = (uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
-#pragma unroll
-      for (int i = 0; i < G::kMWaveLoads; ++i)
-        bload16_lds(rm, sM + (i * WAVES + wave) * 64 * 8, m_off[i] + key0 * 2u);
-    } else {
-#pragma unroll
-      for (int i = 0; i < G::kMWaveLoads; ++i) {
-        const int u = (i * WAVES + wave) * 64 + lane;
-        const int c = (u % 8) ^ mask_swz(u / 8);
-        const int kc = (int)key0 + c * 8;
-        const uint32_t off = m_off[i] + key0 * 2u;
-        if (kc + 8 <= p.sk) {
-          mreg[i] = bload16(rm, off);
-        } else {   // chunk reaching past Sk: element loads, never straddling the buffer end
-          uint32_t w[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t lo = (kc + 2 * j < p.sk)
-                ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j, 0, 0) : 0u;
-            const uint32_t hi = (kc + 2 * j + 1 < p.sk)
-                ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j + 2, 0, 0) : 0u;
-            w[j] = (lo & 0xffffu) | (hi << 16);
-          }
-          mreg[i] = u32x4{w[0], w[1], w[2], w[3]};
-        }
-      }
-    }
-  }
-
-  __device__ __forceinline__ void commit_m(int wave, int lane, uint8_t* smem, int buf) {
-    if constexpr (!MDIRECT) {
-      uint16_t* sM = (uint16_t*)(smem + G::kMOff + buf * G::kMBytes);
-#pragma unroll
-      for (int i = 0; i < G::kMWaveLoads; ++i) {
-        const int u = (i * WAVES + wave) * 64 + lane;
-        *reinterpret_cast<u32x4*>(sM + u * 8) = mreg[i];
-      }
-    }
-  }
-};
 
 template <bool BF16>
 __device__ __forceinline__ f32x16 mask_to_f32(u32x4 lo, u32x4 hi) {
@@ -316,64 +212,230 @@ __device__ __forceinline__ float psum8(typename Elt<BF16>::v8 v, float acc) {
 // result is the same softmax: O and l are always scaled by the same factor.
 constexpr float kRescaleSlack = 5.5451774f;   // 8·ln 2
 
+struct TileIdx {
+  int b, h, hk, split, m0, nb, ne;
+};
+
+template <int BM>
+__device__ __forceinline__ TileIdx tile_index(const KParams& p) {
+  TileIdx ti;
+  int t = xcd_remap(blockIdx.x, p.total);
+  const int mb = t % p.num_m;  t /= p.num_m;
+  ti.split = t % p.num_splits;  t /= p.num_splits;
+  ti.h = t % p.h;
+  ti.b = t / p.h;
+  ti.hk = ti.h / p.ratio;
+  ti.m0 = mb * BM;
+  ti.nb = ti.split * p.n_per_split;
+  ti.ne = min(ti.nb + p.n_per_split, p.num_n);
+  return ti;
+}
+
+// ── main kernel: 32 query rows per wave, WAVES = 4 or 8 waves ─────────────────
+// A wave needs ~250 registers; with 8 waves (BM = 256) two waves share every
+// SIMD, hiding each other's LDS and MFMA latencies. 4 waves (BM = 128) serve
+// small grids and split-KV. K, V and the mask tile arrive by LDS DMA; V is read transposed.
+//  sK   [kBN][D]    unit c of row r at slot c ^ (r % UPR)   (π-permuted rows)
+//  sM   [BM][kBN]   unit u of row m at slot u ^ ((m/2) % 8)
+//  sV   [kBN][D]    natural key order, unit c of row r at slot c ^ swzV(r); the
+//                   PV operand Vᵀ is read with ds_read_b64_tr_b16 (in each 16-lane
+//                   group, source lane s reads 4 d-values of key base + s/4 and
+//                   output lane o receives keys base..base+3 of column D0 + o)
+template <int D, int WAVES> struct Geo {
+  static constexpr int kWaves = WAVES;
+  static constexpr int kBM = 32 * WAVES;
+  static constexpr int kThreads = 64 * WAVES;
+  static constexpr int kUPR = D / 8;
+  static constexpr int kKElems = kBN * D;
+  static constexpr int kMElems = kBM * kBN;
+  static constexpr int kVElems = kBN * D;
+  static constexpr int kKWaveLoads = kBN * kUPR / 64 / kWaves;
+  static constexpr int kMWaveLoads = kBM * 8 / 64 / kWaves;
+};
+
+template <int D> __device__ __forceinline__ int v_swz(int r) {
+  return (D == 128) ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+}
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-template <int D, bool BF16, bool SPLIT, int WAVES, bool MDIRECT>
+__device__ __forceinline__ int mask_swz(int m) { return (m >> 1) & 7; }
+
+template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 struct Attn {
   typedef typename Elt<BF16>::v8 V8;
   typedef Geo<D, WAVES> G;
-  static constexpr int KD = D / 16;  // MFMA k-steps over the head dim
-  static constexpr int DB = D / 32;  // 32-wide d blocks of the output
+  static constexpr int KD = D / 16;
+  static constexpr int DB = D / 32;
 
   const KParams& p;
-  uint8_t* smem;
   int tid, lane, wave, l32, g;
-  int n_begin, n_end;
   rsrc_t rk, rv, rm;
-  Stage<D, WAVES, MDIRECT> st;
+  static constexpr bool mdirect = MDIRECT;
+  uint32_t k_off[G::kKWaveLoads];
+  uint32_t v_off[G::kKWaveLoads];
+  uint32_t m_off[G::kMWaveLoads];
+  uint32_t k_rd[KD];
+  uint32_t v_rd[DB];
+  uint32_t m_rd[4];
   V8 qreg[KD];
   f32x16 oacc[DB];
-  f32x16 s[2];          // Sᵀ of the tile being softmaxed
+  f32x16 s[2];
+  u32x4 mreg[MDIRECT ? 1 : G::kMWaveLoads];
   float m_run, mlog2, l_run;
-  uint32_t k_rd[KD];    // per-lane LDS byte offsets of the K operand reads (buffer 0)
-  uint32_t v_rd[DB];    // per-lane LDS byte offsets of the Vᵀ transpose reads, per d block
-  uint32_t m_rd[4];     // per-lane LDS byte offsets of the mask reads (buffer 0)
 
-  __device__ __forceinline__ Attn(const KParams& p_, uint8_t* smem_) : p(p_), smem(smem_) {}
+  __device__ __forceinline__ Attn(const KParams& p_) : p(p_) {}
 
-  // Sᵀ (two 32-key blocks) for the tile in K buffer KB.
-  template <int KB>
-  __device__ __forceinline__ void qk(f32x16 (&acc)[2]) {
-    acc[0] = f32x16{};
-    acc[1] = f32x16{};
+  __device__ __forceinline__ void init(const TileIdx& ti) {
+    tid = threadIdx.x;
+    lane = tid & 63;
+    wave = tid >> 6;
+    l32 = lane & 31;
+    g = lane >> 5;
+    rk = make_rsrc(p.k + (int64_t)ti.b * p.k_bs + (int64_t)ti.hk * p.k_hs, (uint32_t)p.sk * p.k_rs * 2u);
+    rv = make_rsrc(p.v + (int64_t)ti.b * p.v_bs + (int64_t)ti.hk * p.v_hs, (uint32_t)p.sk * p.v_rs * 2u);
+    rm = make_rsrc(p.mask + (int64_t)ti.b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+#pragma unroll
+    for (int i = 0; i < G::kKWaveLoads; ++i) {
+      const int u = (i * G::kWaves + wave) * 64 + lane;
+      const int r = u / G::kUPR, slot = u % G::kUPR;
+      const int key = (r & ~31) + key_perm(r & 31);
+      k_off[i] = (uint32_t)(key * p.k_rs + (slot ^ (r % G::kUPR)) * 8) * 2u;
+      v_off[i] = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < G::kMWaveLoads; ++i) {
+      const int u = (i * G::kWaves + wave) * 64 + lane;
+      const int m = u / 8, slot = u % 8;
+      m_off[i] = (uint32_t)((ti.m0 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
+    }
+    {
+      // transpose-read source lane s (in its 16-lane group) reads key row
+      // 16g + s/4 (+ a compile-time 32(j/2) + 8(j%2) + 4h), columns
+      // 32·db + 16(group%2) + 4(s%4)
+      const int s16 = lane & 15, grp = lane >> 4;
+      const int row = 16 * g + s16 / 4;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int d = 32 * db + 16 * (grp & 1) + 4 * (s16 & 3);
+        v_rd[db] = (uint32_t)(row * D * 2 + (((d / 8) ^ v_swz<D>(row)) * 16) + (d % 8) * 2);
+      }
+    }
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) {
+      const int c = 2 * kd + g;
+      k_rd[kd] = (uint32_t)(l32 * G::kUPR + (c ^ (l32 % G::kUPR))) * 16u;
+    }
+    const int mr = wave * 32 + l32;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const V8 a = bitcast<V8>(*reinterpret_cast<const u32x4*>(
-            smem + G::kKOff + KB * G::kKBytes + kb * 32 * D * 2 + k_rd[kd]));
-        acc[kb] = Elt<BF16>::mfma(a, qreg[kd], acc[kb]);
+    for (int i = 0; i < 4; ++i) {
+      const int u = (i / 2) * 4 + 2 * g + (i % 2);
+      m_rd[i] = (uint32_t)(mr * kBN + ((u ^ mask_swz(mr)) * 8)) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < DB; ++i) oacc[i] = f32x16{};
+    m_run = -INFINITY;
+    mlog2 = 0.f;
+    l_run = 0.f;
+  }
+
+  __device__ __forceinline__ void load_q(int qrow, rsrc_t rq) {
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd)
+      qreg[kd] = bitcast<V8>(bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u));
+  }
+
+  __device__ __forceinline__ void issue_k(int n, uint16_t* sK) {
+    const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.k_rs * 2u;
+#pragma unroll
+    for (int i = 0; i < G::kKWaveLoads; ++i)
+      bload16_lds(rk, sK + (i * G::kWaves + wave) * 64 * 8, k_off[i] + sh);
+  }
+
+  // Mask tile n: LDS DMA when rows are 16-byte aligned, else registers
+  // (commit_m writes them); chunks reaching past Sk are read element by element.
+  __device__ __forceinline__ void issue_m(int n, uint16_t* sM) {
+    const uint32_t key0 = (uint32_t)n * kBN;
+    if constexpr (MDIRECT) {
+#pragma unroll
+      for (int i = 0; i < G::kMWaveLoads; ++i)
+        bload16_lds(rm, sM + (i * G::kWaves + wave) * 64 * 8, m_off[i] + key0 * 2u);
+      return;
+    } else {
+#pragma unroll
+    for (int i = 0; i < G::kMWaveLoads; ++i) {
+      const int u = (i * G::kWaves + wave) * 64 + lane;
+      const int c = (u % 8) ^ mask_swz(u / 8);
+      const int kc = (int)key0 + c * 8;
+      const uint32_t off = m_off[i] + key0 * 2u;
+      if (kc + 8 <= p.sk) {
+        mreg[i] = bload16(rm, off);
+      } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = (kc + 2 * j < p.sk)
+              ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j, 0, 0) : 0u;
+          const uint32_t hi = (kc + 2 * j + 1 < p.sk)
+              ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j + 2, 0, 0) : 0u;
+          w[j] = (lo & 0xffffu) | (hi << 16);
+        }
+        mreg[i] = u32x4{w[0], w[1], w[2], w[3]};
       }
+    }
     }
   }
 
-  // Softmax of tile n (mask buffer MB) fused with O += Vᵀ·Pᵀ (V buffer MB) and,
-  // when NEXT, Sᵀ of tile n+1 from K buffer MB^1 issued in between.
-  template <int MB, bool NEXT>
-  __device__ __forceinline__ void step(int n) {
-    f32x16 s_next[2];
-    // scores → x = S·scale + mask, natural-log domain
+  __device__ __forceinline__ void commit_m(uint16_t* sM) {
+    if constexpr (MDIRECT) return;
+#pragma unroll
+    for (int i = 0; i < G::kMWaveLoads; ++i) {
+      const int u = (i * G::kWaves + wave) * 64 + lane;
+      *reinterpret_cast<u32x4*>(sM + u * 8) = mreg[i];
+    }
+  }
+
+  __device__ __forceinline__ void issue_v(int n, uint16_t* sV) {
+    const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.v_rs * 2u;
+#pragma unroll
+    for (int i = 0; i < G::kKWaveLoads; ++i)
+      bload16_lds(rv, sV + (i * G::kWaves + wave) * 64 * 8, v_off[i] + sh);
+  }
+
+  // Sᵀ = K·Qᵀ; operands stream through a window of kWin LDS reads in flight.
+  static constexpr int kWin = 2;
+  __device__ __forceinline__ void qk(const uint16_t* sK) {
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+    const uint8_t* kb8 = reinterpret_cast<const uint8_t*>(sK);
+    constexpr int N = 2 * KD;   // step i: kd = i / 2, kb = i % 2
+    auto rd = [&](int i) {
+      return bitcast<V8>(*reinterpret_cast<const u32x4*>(kb8 + (i % 2) * 32 * D * 2 + k_rd[i / 2]));
+    };
+    V8 win[kWin];
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) win[i] = rd(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const V8 a = win[i % kWin];
+      if (i + kWin < N) win[i % kWin] = rd(i + kWin);
+      s[i % 2] = Elt<BF16>::mfma(a, qreg[i / 2], s[i % 2]);
+    }
+  }
+
+  // softmax of tile n and Oᵀ += Vᵀ·Pᵀ, the exponentials of each key step one
+  // step ahead of its MFMAs
+  __device__ __forceinline__ void softmax_pv(const uint16_t* sM, const uint16_t* sVt, int n) {
+    const uint8_t* mb = reinterpret_cast<const uint8_t*>(sM);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const uint8_t* mb = smem + G::kMOff + MB * G::kMBytes;
       const u32x4 lo = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * kb]);
       const u32x4 hi = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * kb + 1]);
       const f32x16 mk = mask_to_f32<BF16>(lo, hi);
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kb][i] = __builtin_fmaf(s[kb][i], p.scale, mk[i]);
     }
-    if constexpr (NEXT) qk<MB ^ 1>(s_next);
     if ((n + 1) * kBN > p.sk) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -389,172 +451,147 @@ struct Attn {
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
     mx = xhalf_max(mx);
-
     const bool need = mx > m_run + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(need)) {
       // lanes that keep their max scale by exactly 1 (also avoids -inf - -inf)
-      const float alpha = need ? __builtin_amdgcn_exp2f((m_run - mx) * kLog2e) : 1.f;  // -inf → 0
+      const float alpha = need ? __builtin_amdgcn_exp2f((m_run - mx) * kLog2e) : 1.f;
       m_run = need ? mx : m_run;
       mlog2 = (m_run == -INFINITY) ? 0.f : m_run * kLog2e;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
     }
+    // PV operands (step i: key step j = i / DB, d block db = i % DB) stream
+    // through a window of kWin LDS reads in flight.
+    constexpr int N = 4 * DB;
+    const uint8_t* vb = reinterpret_cast<const uint8_t*>(sVt);
+    auto rd = [&](int i) {
+      const int j = i / DB, db = i % DB;
+      const int off = ((j / 2) * 32 + (j % 2) * 8) * D * 2;
+      const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + v_rd[db] + off));
+      const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(vb + v_rd[db] + off + 4 * D * 2));
+      return bitcast<V8>(__builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    V8 win[kWin];
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) win[i] = rd(i);
+    V8 pb;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int j = i / DB;
+      if (i % DB == 0) {
+        f32x8 pf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pf[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j / 2][(j % 2) * 8 + e], kLog2e, -mlog2));
+        pb = __builtin_convertvector(pf, V8);
+        l_run = psum8<BF16>(pb, l_run);
+      }
+      const V8 a = win[i % kWin];
+      if (i + kWin < N) win[i % kWin] = rd(i + kWin);
+      oacc[i % DB] = Elt<BF16>::mfma(a, pb, oacc[i % DB]);
+    }
+  }
 
-    // P = exp(x − m) rounded to the dtype; Oᵀ += Vᵀ·Pᵀ one 16-key step at a time
-    const uint8_t* vb = smem + G::kVOff + MB * G::kKBytes;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      f32x8 pf;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j / 2][(j % 2) * 8 + i], kLog2e, -mlog2));
-      const V8 pb = __builtin_convertvector(pf, V8);
-      l_run = psum8<BF16>(pb, l_run);
+  __device__ __forceinline__ void epilogue(int b, int h, int split, int qrow) {
+    const float l = xhalf_sum(l_run);
+    const float inv = (l == 0.f || l != l) ? 1.f : 1.f / l;
+    if constexpr (!SPLIT) {
+      const rsrc_t ro = make_rsrc(p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs,
+                                  (uint32_t)p.sq * p.o_rs * 2u);
+      const uint32_t obase = (uint32_t)(qrow * p.o_rs + g * 4) * 2u;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        // rows (keys) 32(j/2) + 16g + 8(j%2) + [0,8) of Vᵀ column db·32 + l32
-        const int off = ((j / 2) * 32 + (j % 2) * 8) * D * 2;
-        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + v_rd[db] + off));
-        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(vb + v_rd[db] + off + 4 * D * 2));
-        const V8 a = bitcast<V8>(__builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
-        oacc[db] = Elt<BF16>::mfma(a, pb, oacc[db]);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          f32x4 v4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
+          typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+          typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+          u32x2 packed;
+          if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
+          else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
+          __builtin_amdgcn_raw_buffer_store_b64(packed, ro, obase + (db * 32 + q4 * 8) * 2u, 0, 0);
+        }
       }
-    }
-    if constexpr (NEXT) {
-      s[0] = s_next[0];
-      s[1] = s_next[1];
+    } else {
+      if (qrow >= p.sq) return;
+      const int64_t bh = (int64_t)b * p.h + h;
+      const int64_t slab = (int64_t)p.b * p.h * p.sq;
+      const int64_t prow = (int64_t)split * slab + bh * p.sq + qrow;
+      float* op = p.o_part + prow * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          f32x4 v4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
+          *reinterpret_cast<f32x4*>(op + db * 32 + q4 * 8 + g * 4) = v4;
+        }
+      }
+      if (g == 0)
+        p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY
+                                                 : m_run + __builtin_amdgcn_logf(l) * 0.69314718f;
     }
   }
 };
 
-// PIPE = software-pipelined QKᵀ(n+1) under softmax(n); used with one wave per
-// SIMD (4 waves), where the wave has the whole 512-entry register file.
-template <int D, bool BF16, bool SPLIT, int WAVES, bool MDIRECT>
+// Iteration over tile n (parity P): K(n), mask(n), Vᵀ(n) are in buffers P.
+//   issue K(n+1), mask(n+1) → buffers P^1 (LDS DMA), V(n+1) → registers;
+//   Sᵀ(n) = K(n)·Qᵀ; softmax(n) fused with Oᵀ += Vᵀ(n)·Pᵀ(n);
+//   V(n+1) → Vᵀ buffer P^1.  One barrier per iteration.
+template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
-  constexpr bool PIPE = (WAVES == 4);
-  typedef Attn<D, BF16, SPLIT, WAVES, MDIRECT> A;
   typedef Geo<D, WAVES> G;
-  typedef typename A::V8 V8;
-  constexpr int kBM = G::kBM;
-  constexpr int DB = A::DB;
+  typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
+  __shared__ __align__(16) uint16_t sK0[G::kKElems], sK1[G::kKElems];
+  __shared__ __align__(16) uint16_t sM0[G::kMElems], sM1[G::kMElems];
+  __shared__ __align__(16) uint16_t sV0[G::kVElems], sV1[G::kVElems];
 
-  extern __shared__ __align__(16) uint8_t smem[];
-  A a(p, smem);
-  a.tid = threadIdx.x;
-  a.lane = a.tid & 63;
-  a.wave = a.tid >> 6;
-  a.l32 = a.lane & 31;
-  a.g = a.lane >> 5;
-  const int lane = a.lane, wave = a.wave, l32 = a.l32, g = a.g;
-
-  // logical tile id → (b, h, split, m_block)
-  int t = xcd_remap(blockIdx.x, p.total);
-  const int mb = t % p.num_m;  t /= p.num_m;
-  const int split = t % p.num_splits;  t /= p.num_splits;
-  const int h = t % p.h;
-  const int b = t / p.h;
-  const int hk = h / p.ratio;
-
-  const int m0 = mb * kBM;
-  const int nb = split * p.n_per_split;
-  const int ne = min(nb + p.n_per_split, p.num_n);
-
-  const rsrc_t rq = make_rsrc(p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs,
+  const TileIdx ti = tile_index<G::kBM>(p);
+  A a(p);
+  a.init(ti);
+  const int nb = ti.nb, ne = ti.ne;
+  const rsrc_t rq = make_rsrc(p.q + (int64_t)ti.b * p.q_bs + (int64_t)ti.h * p.q_hs,
                               (uint32_t)p.sq * p.q_rs * 2u);
-  a.rk = make_rsrc(p.k + (int64_t)b * p.k_bs + (int64_t)hk * p.k_hs, (uint32_t)p.sk * p.k_rs * 2u);
-  a.rv = make_rsrc(p.v + (int64_t)b * p.v_bs + (int64_t)hk * p.v_hs, (uint32_t)p.sk * p.v_rs * 2u);
-  a.rm = make_rsrc(p.mask + (int64_t)b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
-
-  // per-lane LDS read offsets (buffer 0; other buffers are compile-time shifts)
-#pragma unroll
-  for (int kd = 0; kd < A::KD; ++kd) {
-    const int c = 2 * kd + g;
-    a.k_rd[kd] = (uint32_t)(l32 * G::kUPR + (c ^ (l32 % G::kUPR))) * 16u;
-  }
-  {
-    // ds_read_b64_tr_b16: in each 16-lane group, source lane s supplies 4 d-values
-    // of key base + s/4 and output lane o receives keys base..base+3 of column
-    // D0 + o. Source lane s therefore reads key row 16g + s/4 (+ a compile-time
-    // 32(j/2) + 8(j%2) + 4h, a multiple of 4), columns 32·db + 16(group%2) + 4(s%4).
-    const int s16 = lane & 15, grp = lane >> 4;
-    const int row = 16 * g + s16 / 4;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const int d = 32 * db + 16 * (grp & 1) + 4 * (s16 & 3);
-      a.v_rd[db] = (uint32_t)(row * D * 2 + (((d / 8) ^ v_swz<D>(row)) * 16) + (d % 8) * 2);
-    }
-  }
-  {
-    const int mr = wave * 32 + l32;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = (i / 2) * 4 + 2 * g + (i % 2);           // units of keys kb·32 + 16g + 8(i%2)
-      a.m_rd[i] = (uint32_t)(mr * kBN + ((u ^ mask_swz(mr)) * 8)) * 2u;
-    }
-  }
-
-  a.st.init(p, wave, lane, m0);
-  // Zero both V buffers once: a V row the tail's DMA leaves unwritten then holds
+  const int qrow = ti.m0 + a.wave * 32 + a.l32;
+  // Zero the V buffers once: a V row the tail's DMA leaves unwritten then holds
   // 0 or an earlier tile's finite values, and its P is 0, so it adds nothing.
-  for (int i = a.tid; i < 2 * G::kKBytes / 16; i += G::kThreads)
-    *reinterpret_cast<u32x4*>(smem + G::kVOff + i * 16) = u32x4{0u, 0u, 0u, 0u};
+  for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads) {
+    reinterpret_cast<u32x4*>(sV0)[i] = u32x4{0u, 0u, 0u, 0u};
+    reinterpret_cast<u32x4*>(sV1)[i] = u32x4{0u, 0u, 0u, 0u};
+  }
   __syncthreads();
   if (nb < ne) {
-    a.st.issue_k(p, nb, wave, smem, 0, a.rk);
-    a.st.issue_v(p, nb, wave, smem, 0, a.rv);
-    a.st.issue_m(p, nb, wave, lane, smem, 0, a.rm);
-    if (PIPE && nb + 1 < ne) a.st.issue_k(p, nb + 1, wave, smem, 1, a.rk);
+    a.issue_k(nb, sK0);
+    a.issue_m(nb, sM0);
+    a.issue_v(nb, sV0);
   }
+  a.load_q(qrow, rq);
+  if (nb < ne) a.commit_m(sM0);
 
-  // Q for this lane's row, as the B operand of Sᵀ = K·Qᵀ (kept for the whole loop).
-  const int qrow = m0 + wave * 32 + l32;
-#pragma unroll
-  for (int kd = 0; kd < A::KD; ++kd)
-    a.qreg[kd] = bitcast<V8>(bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u));
-
-#pragma unroll
-  for (int i = 0; i < DB; ++i) a.oacc[i] = f32x16{};
-  a.m_run = -INFINITY;
-  a.mlog2 = 0.f;
-  a.l_run = 0.f;
-
-  if (nb < ne) a.st.commit_m(wave, lane, smem, 0);
-  if (PIPE && nb < ne) {
-    wait_vmem();
-    __syncthreads();
-    a.template qk<0>(a.s);
-  }
-
-  // Iteration over tile n (parity P = (n - nb) % 2, compile-time): mask(n) and
-  // V(n) sit in buffer P; tile n+1's mask/V (and K) go to the buffers the
-  // previous iteration finished reading.
-  //  PIPE:  K(n+1) is already in K buffer P^1 and K(n+2) is prefetched into P;
-  //         Sᵀ(n+1) is computed while tile n is softmaxed.
-  //  !PIPE: K(n) is in K buffer P; K(n+1) is prefetched into P^1.
   auto iter = [&](auto parity, int n) {
     constexpr int P = decltype(parity)::value;
-    wait_vmem();
+    uint16_t* kH = P ? sK1 : sK0;
+    uint16_t* kN = P ? sK0 : sK1;
+    uint16_t* mH = P ? sM1 : sM0;
+    uint16_t* mN = P ? sM0 : sM1;
+    uint16_t* vH = P ? sV1 : sV0;
+    uint16_t* vN = P ? sV0 : sV1;
+    wait_vmcnt<0>();
     __syncthreads();
     const bool more = n + 1 < ne;
-    if constexpr (PIPE) {
-      if (n + 2 < ne) a.st.issue_k(p, n + 2, wave, smem, P, a.rk);
-    } else {
-      if (more) a.st.issue_k(p, n + 1, wave, smem, P ^ 1, a.rk);
-    }
     if (more) {
-      a.st.issue_v(p, n + 1, wave, smem, P ^ 1, a.rv);
-      a.st.issue_m(p, n + 1, wave, lane, smem, P ^ 1, a.rm);
+      a.issue_k(n + 1, kN);
+      a.issue_m(n + 1, mN);
+      a.issue_v(n + 1, vN);
     }
-    if constexpr (PIPE) {
-      if (more) a.template step<P, true>(n);
-      else a.template step<P, false>(n);
-    } else {
-      a.template qk<P>(a.s);
-      a.template step<P, false>(n);
-    }
-    if (more) a.st.commit_m(wave, lane, smem, P ^ 1);
+    a.qk(kH);
+    a.softmax_pv(mH, vH, n);
+    if (more) a.commit_m(mN);
   };
   int n = nb;
   for (; n + 1 < ne; n += 2) {
@@ -563,51 +600,7 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   }
   if (n < ne) iter(std::integral_constant<int, 0>{}, n);
 
-  // ── epilogue ────────────────────────────────────────────────────────────
-  const float l = xhalf_sum(a.l_run);
-  const float inv = (l == 0.f || l != l) ? 1.f : 1.f / l;
-
-  if constexpr (!SPLIT) {
-    const rsrc_t ro = make_rsrc(p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs,
-                                (uint32_t)p.sq * p.o_rs * 2u);
-    const uint32_t obase = (uint32_t)(qrow * p.o_rs + g * 4) * 2u;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        f32x4 v4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = a.oacc[db][q4 * 4 + i] * inv;
-        typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-        typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
-        u32x2 packed;
-        if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
-        else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
-        __builtin_amdgcn_raw_buffer_store_b64(packed, ro, obase + (db * 32 + q4 * 8) * 2u, 0, 0);
-      }
-    }
-  } else {
-    if (qrow >= p.sq) return;
-    const int64_t bh = (int64_t)b * p.h + h;
-    const int64_t slab = (int64_t)p.b * p.h * p.sq;   // rows per split
-    const int64_t prow = (int64_t)split * slab + bh * p.sq + qrow;
-    float* op = p.o_part + prow * D;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        f32x4 v4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = a.oacc[db][q4 * 4 + i] * inv;
-        *reinterpret_cast<f32x4*>(op + db * 32 + q4 * 8 + g * 4) = v4;
-      }
-    }
-    if (g == 0) {
-      // natural-log LSE of this split's row (reference convention lse = m + log l)
-      p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY
-                                               : a.m_run + __builtin_amdgcn_logf(l) * 0.69314718f;
-    }
-  }
+  a.epilogue(ti.b, ti.h, ti.split, qrow);
 }
 
 // ── split-KV combine ────────────────────────────────────────────────────────
@@ -760,8 +753,9 @@ struct Plan {
   size_t o_part_bytes, lse_bytes, ws_bytes;
 };
 
-// Tile plan: 8 waves × 32 rows (BM = 256) when that grid fills the chip,
-// otherwise BM = 128 (4 waves), and split-KV when even that under-fills it.
+// Tile plan. BM = 256 rows (8 waves) when that grid fills the chip; otherwise
+// BM = 128 (4 waves), with split-KV chosen by the cost model when even that
+// grid leaves CUs idle.
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
   pl.num_n = ceil_div(p->seqlen_k, kBN);
@@ -772,21 +766,16 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
     if (env && atoi(env) > 0) s = atoi(env);
   }
   const int m256 = ceil_div(p->seqlen_q, 256), m128 = ceil_div(p->seqlen_q, 128);
-  if (s <= 0) {
-    if ((float)bh * m256 >= 0.8f * cus) {
-      s = 1;
-    } else {
-      s = cost_model_splits(bh * m128, pl.num_n, 128, p->d, cus);
-    }
-  }
+  const bool big = (float)bh * m256 >= 0.8f * cus;
+  if (s <= 0) s = big ? 1 : cost_model_splits(bh * m128, pl.num_n, 128, p->d, cus);
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > pl.num_n) s = pl.num_n;
   if (s < 1) s = 1;
   pl.splits = s;
-  pl.waves = (s == 1 && (float)bh * m256 >= 0.8f * cus) ? 8 : 4;
-  if (s == 1) {   // tuning override; split-KV always uses the 4-wave kernel
-    const char* wenv = getenv("MI355_FA_WAVES");
-    if (wenv && (atoi(wenv) == 4 || atoi(wenv) == 8)) pl.waves = atoi(wenv);
+  pl.waves = (s == 1 && big) ? 8 : 4;
+  {   // tuning override of the workgroup size (4 or 8 waves)
+    const char* w = getenv("MI355_FA_WAVES");
+    if (w && (atoi(w) == 4 || atoi(w) == 8)) pl.waves = atoi(w);
   }
   pl.block_m = 32 * pl.waves;
   pl.num_m = ceil_div(p->seqlen_q, pl.block_m);
@@ -849,39 +838,32 @@ static int validate(const mi355_fa_params* p, char* err, size_t errlen) {
   return MI355_FA_OK;
 }
 
-template <int D, bool BF16, bool SPLIT, int WAVES, bool MDIRECT>
+template <int D, bool BF16, bool SPLIT, int WAVES>
 static hipError_t launch_main(const KParams& kp, hipStream_t st) {
-  auto kern = fa_fwd_kernel<D, BF16, SPLIT, WAVES, MDIRECT>;
-  constexpr int smem = Geo<D, WAVES>::kBytes;
-  static std::once_flag once;
-  static hipError_t attr_err = hipSuccess;
-  std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-  });
-  if (attr_err != hipSuccess) return attr_err;
-  hipLaunchKernelGGL(kern, dim3(kp.total), dim3(64 * WAVES), smem, st, kp);
+  if (kp.mask_direct)
+    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, true, WAVES>), dim3(kp.total),
+                       dim3(64 * WAVES), 0, st, kp);
+  else
+    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, false, WAVES>), dim3(kp.total),
+                       dim3(64 * WAVES), 0, st, kp);
   return hipGetLastError();
 }
 
+template <int D, bool BF16, bool SPLIT>
+static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t st) {
+  return pl.waves == 8 ? launch_main<D, BF16, SPLIT, 8>(kp, st)
+                       : launch_main<D, BF16, SPLIT, 4>(kp, st);
+}
+
 template <int D, bool BF16>
-static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, bool mdirect,
-                         hipStream_t st) {
-  hipError_t e;
-  if (pl.splits > 1) {
-    e = mdirect ? launch_main<D, BF16, true, 4, true>(kp, st)
-                : launch_main<D, BF16, true, 4, false>(kp, st);
-    if (e != hipSuccess) return e;
-    constexpr int kRows = 256 / (D / 4);
-    const int64_t blocks = (cp.rows + kRows - 1) / kRows;
-    hipLaunchKernelGGL((fa_combine_kernel<D, BF16>), dim3((unsigned)blocks), dim3(256), 0, st, cp);
-    return hipGetLastError();
-  }
-  if (pl.waves == 8)
-    return mdirect ? launch_main<D, BF16, false, 8, true>(kp, st)
-                   : launch_main<D, BF16, false, 8, false>(kp, st);
-  return mdirect ? launch_main<D, BF16, false, 4, true>(kp, st)
-                 : launch_main<D, BF16, false, 4, false>(kp, st);
+static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, hipStream_t st) {
+  if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
+  hipError_t e = launch_variant<D, BF16, true>(kp, pl, st);
+  if (e != hipSuccess) return e;
+  constexpr int kRows = 256 / (D / 4);
+  const int64_t blocks = (cp.rows + kRows - 1) / kRows;
+  hipLaunchKernelGGL((fa_combine_kernel<D, BF16>), dim3((unsigned)blocks), dim3(256), 0, st, cp);
+  return hipGetLastError();
 }
 
 }  // namespace mi355fa
@@ -893,7 +875,7 @@ extern "C" {
 int mi355_fa_abi_version(void) { return MI355_FA_ABI_VERSION; }
 
 const char* mi355_fa_build_info(void) {
-  return "mi355_fa gfx950 BM=128/256 BN=64 waves=4/8 mfma32x32x16 lds-dma splitkv+combine";
+  return "mi355_fa gfx950 BM=128/256 BN=64 32-rows/wave mfma32x32x16 lds-dma tr-reads splitkv+combine";
 }
 
 int mi355_fa_cost_model_splits(int total_mblocks, int num_n_blocks, int block_m, int head_dim,
@@ -966,6 +948,8 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.num_splits = pl.splits; kp.n_per_split = pl.n_per_split;
   kp.total = (int)total;
   kp.scale = p->scale_softmax;
+  kp.mask_direct = (((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
+                    (p->mask_row_stride & 7) == 0) ? 1 : 0;
 
   CParams cp{};
   if (split) {
@@ -982,12 +966,10 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   const bool bf16 = p->dtype == MI355_FA_BF16;
-  const bool mdirect = ((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
-                       (p->mask_row_stride & 7) == 0;
   if (p->d == 128)
-    e = bf16 ? launch<128, true>(kp, cp, pl, mdirect, st) : launch<128, false>(kp, cp, pl, mdirect, st);
+    e = bf16 ? launch<128, true>(kp, cp, pl, st) : launch<128, false>(kp, cp, pl, st);
   else
-    e = bf16 ? launch<64, true>(kp, cp, pl, mdirect, st) : launch<64, false>(kp, cp, pl, mdirect, st);
+    e = bf16 ? launch<64, true>(kp, cp, pl, st) : launch<64, false>(kp, cp, pl, st);
   if (e != hipSuccess) {
     set_err(err, errlen, "mi355_fa launch failed: %s", hipGetErrorString(e));
     return MI355_FA_ELAUNCH;

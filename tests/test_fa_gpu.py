@@ -181,6 +181,22 @@ def test_split_invariance(ops, gpu, splits):
     assert torch.all(out[:, :, 5, :] == 0)
 
 
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp16"])
+@pytest.mark.parametrize("sk,extra_cols", [(1000, 0), (777, 3)])
+def test_workgroup_variants(ops, gpu, monkeypatch, waves, splits, d, dtype, sk, extra_cols):
+    """Both workgroup sizes (4 waves / BM 128, 8 waves / BM 256), forced through
+    the single-pass and split-KV epilogues, with 16-byte-aligned mask rows (LDS
+    DMA) and unaligned ones (register path)."""
+    monkeypatch.setenv("MI355_FA_WAVES", str(waves))
+    case = make_case(2, 4, 2, 300, sk, d, "inf_random", dtype, extra_cols=extra_cols)
+    case[3][1, :, 17, :] = float("-inf")
+    out, _ = run(ops, case, gpu, f"w{waves} s{splits} d{d} sk{sk}", num_splits=splits)
+    assert torch.all(out[1, :, 17, :] == 0)
+
+
 def test_all_masked_everything_split(ops, gpu):
     q, k, v, m = make_case(1, 2, 2, 64, 4096, 128, "zero", torch.bfloat16)
     m = torch.full_like(m, float("-inf"))
