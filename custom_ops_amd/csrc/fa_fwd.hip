@@ -89,8 +89,10 @@ __device__ __forceinline__ To bitcast(const From& x) {
 // Raw buffer loads/stores with 32-bit offsets: the hardware returns 0 for reads
 // (and drops writes) at offsets >= num_records. Each resource is bounded to the
 // valid rows of one head / one batch, so K/V rows >= Sk, Q/O rows >= Sq and mask
-// rows >= mask_seqlen_q need no predicate. All variable offsets are passed as the
-// per-lane (VGPR) offset, which is what the range check covers.
+// rows >= mask_seqlen_q need no predicate. All variable per-lane offsets are
+// passed as the VGPR offset, which is what the range check covers; the per-tile
+// shift along the keys moves the resource base instead (scalar arithmetic),
+// shrinking num_records by the same amount so the check is unchanged.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef __attribute__((address_space(3))) void lds_void;
 constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
@@ -134,6 +136,7 @@ struct KParams {
   int n_per_split;   // tiles per split
   int total;         // grid size (workgroups)
   int mask_direct;   // mask rows 16-byte aligned: the mask tile can go by LDS DMA
+  int head_major;    // tile order: heads fastest (else m-blocks fastest)
   float scale;       // softmax scale (1/sqrt(d) in the reference op)
 };
 
@@ -220,10 +223,18 @@ template <int BM>
 __device__ __forceinline__ TileIdx tile_index(const KParams& p) {
   TileIdx ti;
   int t = xcd_remap(blockIdx.x, p.total);
-  const int mb = t % p.num_m;  t /= p.num_m;
-  ti.split = t % p.num_splits;  t /= p.num_splits;
-  ti.h = t % p.h;
-  ti.b = t / p.h;
+  int mb;
+  if (p.head_major) {   // (b, split, m-block, h): the heads sharing a mask tile run together
+    ti.h = t % p.h;  t /= p.h;
+    mb = t % p.num_m;  t /= p.num_m;
+    ti.split = t % p.num_splits;
+    ti.b = t / p.num_splits;
+  } else {              // (b, h, split, m-block): the m-blocks sharing K/V run together
+    mb = t % p.num_m;  t /= p.num_m;
+    ti.split = t % p.num_splits;  t /= p.num_splits;
+    ti.h = t % p.h;
+    ti.b = t / p.h;
+  }
   ti.hk = ti.h / p.ratio;
   ti.m0 = mb * BM;
   ti.nb = ti.split * p.n_per_split;
@@ -271,7 +282,9 @@ struct Attn {
 
   const KParams& p;
   int tid, lane, wave, l32, g;
-  rsrc_t rk, rv, rm;
+  const uint16_t *kbase, *vbase, *mbase;
+  uint32_t kbytes, vbytes, mbytes;
+  rsrc_t rm;
   static constexpr bool mdirect = MDIRECT;
   uint32_t k_off[G::kKWaveLoads];
   uint32_t v_off[G::kKWaveLoads];
@@ -290,12 +303,16 @@ struct Attn {
   __device__ __forceinline__ void init(const TileIdx& ti) {
     tid = threadIdx.x;
     lane = tid & 63;
-    wave = tid >> 6;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     l32 = lane & 31;
     g = lane >> 5;
-    rk = make_rsrc(p.k + (int64_t)ti.b * p.k_bs + (int64_t)ti.hk * p.k_hs, (uint32_t)p.sk * p.k_rs * 2u);
-    rv = make_rsrc(p.v + (int64_t)ti.b * p.v_bs + (int64_t)ti.hk * p.v_hs, (uint32_t)p.sk * p.v_rs * 2u);
-    rm = make_rsrc(p.mask + (int64_t)ti.b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+    kbase = p.k + (int64_t)ti.b * p.k_bs + (int64_t)ti.hk * p.k_hs;
+    vbase = p.v + (int64_t)ti.b * p.v_bs + (int64_t)ti.hk * p.v_hs;
+    mbase = p.mask + (int64_t)ti.b * p.m_bs;
+    kbytes = (uint32_t)p.sk * p.k_rs * 2u;
+    vbytes = (uint32_t)p.sk * p.v_rs * 2u;
+    mbytes = (uint32_t)p.msq * p.m_rs * 2u;
+    rm = make_rsrc(mbase, mbytes);
 #pragma unroll
     for (int i = 0; i < G::kKWaveLoads; ++i) {
       const int u = (i * G::kWaves + wave) * 64 + lane;
@@ -348,9 +365,10 @@ struct Attn {
 
   __device__ __forceinline__ void issue_k(int n, uint16_t* sK) {
     const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.k_rs * 2u;
+    const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(kbase) + sh, kbytes - sh);
 #pragma unroll
     for (int i = 0; i < G::kKWaveLoads; ++i)
-      bload16_lds(rk, sK + (i * G::kWaves + wave) * 64 * 8, k_off[i] + sh);
+      bload16_lds(r, sK + (i * G::kWaves + wave) * 64 * 8, k_off[i]);
   }
 
   // Mask tile n: LDS DMA when rows are 16-byte aligned, else registers
@@ -358,9 +376,10 @@ struct Attn {
   __device__ __forceinline__ void issue_m(int n, uint16_t* sM) {
     const uint32_t key0 = (uint32_t)n * kBN;
     if constexpr (MDIRECT) {
+      const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(mbase) + key0 * 2u, mbytes - key0 * 2u);
 #pragma unroll
       for (int i = 0; i < G::kMWaveLoads; ++i)
-        bload16_lds(rm, sM + (i * G::kWaves + wave) * 64 * 8, m_off[i] + key0 * 2u);
+        bload16_lds(r, sM + (i * G::kWaves + wave) * 64 * 8, m_off[i]);
       return;
     } else {
 #pragma unroll
@@ -398,9 +417,10 @@ struct Attn {
 
   __device__ __forceinline__ void issue_v(int n, uint16_t* sV) {
     const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.v_rs * 2u;
+    const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(vbase) + sh, vbytes - sh);
 #pragma unroll
     for (int i = 0; i < G::kKWaveLoads; ++i)
-      bload16_lds(rv, sV + (i * G::kWaves + wave) * 64 * 8, v_off[i] + sh);
+      bload16_lds(r, sV + (i * G::kWaves + wave) * 64 * 8, v_off[i]);
   }
 
   // Sᵀ = K·Qᵀ; operands stream through a window of kWin LDS reads in flight.
@@ -424,9 +444,8 @@ struct Attn {
     }
   }
 
-  // softmax of tile n and Oᵀ += Vᵀ·Pᵀ, the exponentials of each key step one
-  // step ahead of its MFMAs
-  __device__ __forceinline__ void softmax_pv(const uint16_t* sM, const uint16_t* sVt, int n) {
+  // scores of tile n: S·scale + mask, keys past Sk → -inf
+  __device__ __forceinline__ void add_mask(const uint16_t* sM, int n) {
     const uint8_t* mb = reinterpret_cast<const uint8_t*>(sM);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -445,6 +464,11 @@ struct Attn {
           s[kb][i] = (key < p.sk) ? s[kb][i] : -INFINITY;
         }
     }
+  }
+
+  // softmax of tile n and Oᵀ += Vᵀ·Pᵀ, the exponentials of each key step one
+  // step ahead of its MFMAs
+  __device__ __forceinline__ void softmax_pv(const uint16_t* sVt) {
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -539,17 +563,37 @@ struct Attn {
   }
 };
 
-// Iteration over tile n (parity P): K(n), mask(n), Vᵀ(n) are in buffers P.
-//   issue K(n+1), mask(n+1) → buffers P^1 (LDS DMA), V(n+1) → registers;
-//   Sᵀ(n) = K(n)·Qᵀ; softmax(n) fused with Oᵀ += Vᵀ(n)·Pᵀ(n);
-//   V(n+1) → Vᵀ buffer P^1.  One barrier per iteration.
+template <int I>
+__device__ __forceinline__ uint16_t* stage_buf(uint16_t* b0, uint16_t* b1, uint16_t* b2) {
+  if constexpr (I == 0) return b0;
+  else if constexpr (I == 1) return b1;
+  else return b2;
+}
+
+// Software pipeline over KV tiles with NS LDS stages (2 or 3).
+// Iteration over tile n, stage ST = (n - nb) % NS holding K(n), V(n), mask(n):
+//   wait until tile n's loads have landed (tiles n+1 .. n+NS-2 may still be in
+//   flight) + barrier; issue K, V, mask of tile n+NS-1 into the stage freed by
+//   tile n-1; Sᵀ(n) = K(n)·Qᵀ; + mask(n); softmax(n) fused with
+//   Oᵀ += Vᵀ(n)·Pᵀ(n). One barrier per tile.
+// Unaligned mask rows go through registers one tile ahead instead (loaded
+// before the DMAs so waiting for them does not wait for the DMAs).
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
   typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
+  // 3 stages measured no faster than 2 for the 4-wave kernel (cfg4/cfg5 shapes)
+  // and cost 48 KiB of LDS, so both variants run 2 stages.
+  constexpr int NS = 2;
+  // LDS-DMA instructions per wave per tile
+  constexpr int kL = 2 * G::kKWaveLoads + (MDIRECT ? G::kMWaveLoads : 0);
+  static_assert(kL * (NS - 2) < 64, "vmcnt range");
   __shared__ __align__(16) uint16_t sK0[G::kKElems], sK1[G::kKElems];
-  __shared__ __align__(16) uint16_t sM0[G::kMElems], sM1[G::kMElems];
   __shared__ __align__(16) uint16_t sV0[G::kVElems], sV1[G::kVElems];
+  __shared__ __align__(16) uint16_t sM0[G::kMElems], sM1[G::kMElems];
+  __shared__ __align__(16) uint16_t sK2[NS == 3 ? G::kKElems : 8];
+  __shared__ __align__(16) uint16_t sV2[NS == 3 ? G::kVElems : 8];
+  __shared__ __align__(16) uint16_t sM2[NS == 3 ? G::kMElems : 8];
 
   const TileIdx ti = tile_index<G::kBM>(p);
   A a(p);
@@ -563,42 +607,67 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads) {
     reinterpret_cast<u32x4*>(sV0)[i] = u32x4{0u, 0u, 0u, 0u};
     reinterpret_cast<u32x4*>(sV1)[i] = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (NS == 3) reinterpret_cast<u32x4*>(sV2)[i] = u32x4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
+  // prologue: tiles nb .. nb+NS-2
   if (nb < ne) {
-    a.issue_k(nb, sK0);
     a.issue_m(nb, sM0);
+    a.issue_k(nb, sK0);
     a.issue_v(nb, sV0);
+  }
+  if constexpr (NS == 3) {
+    if (nb + 1 < ne) {
+      if constexpr (MDIRECT) a.issue_m(nb + 1, sM1);
+      a.issue_k(nb + 1, sK1);
+      a.issue_v(nb + 1, sV1);
+    }
   }
   a.load_q(qrow, rq);
   if (nb < ne) a.commit_m(sM0);
 
-  auto iter = [&](auto parity, int n) {
-    constexpr int P = decltype(parity)::value;
-    uint16_t* kH = P ? sK1 : sK0;
-    uint16_t* kN = P ? sK0 : sK1;
-    uint16_t* mH = P ? sM1 : sM0;
-    uint16_t* mN = P ? sM0 : sM1;
-    uint16_t* vH = P ? sV1 : sV0;
-    uint16_t* vN = P ? sV0 : sV1;
-    wait_vmcnt<0>();
-    __syncthreads();
-    const bool more = n + 1 < ne;
-    if (more) {
-      a.issue_k(n + 1, kN);
-      a.issue_m(n + 1, mN);
-      a.issue_v(n + 1, vN);
+  auto iter = [&](auto stc, int n) {
+    constexpr int ST = decltype(stc)::value;
+    constexpr int NX = (ST + NS - 1) % NS;   // receives tile n+NS-1
+    constexpr int N1 = (ST + 1) % NS;        // holds tile n+1
+    if constexpr (NS == 3) {
+      if (n + 1 < ne) wait_vmcnt<kL>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
     }
-    a.qk(kH);
-    a.softmax_pv(mH, vH, n);
-    if (more) a.commit_m(mN);
+    __syncthreads();
+    if constexpr (!MDIRECT) {
+      if (n + 1 < ne) a.issue_m(n + 1, nullptr);   // into registers
+    }
+    if (n + NS - 1 < ne) {
+      if constexpr (MDIRECT) a.issue_m(n + NS - 1, stage_buf<NX>(sM0, sM1, sM2));
+      a.issue_k(n + NS - 1, stage_buf<NX>(sK0, sK1, sK2));
+      a.issue_v(n + NS - 1, stage_buf<NX>(sV0, sV1, sV2));
+    }
+    a.qk(stage_buf<ST>(sK0, sK1, sK2));
+    a.add_mask(stage_buf<ST>(sM0, sM1, sM2), n);
+    a.softmax_pv(stage_buf<ST>(sV0, sV1, sV2));
+    if constexpr (!MDIRECT) {
+      if (n + 1 < ne) a.commit_m(stage_buf<N1>(sM0, sM1, sM2));
+    }
   };
   int n = nb;
-  for (; n + 1 < ne; n += 2) {
-    iter(std::integral_constant<int, 0>{}, n);
-    iter(std::integral_constant<int, 1>{}, n + 1);
+  if constexpr (NS == 3) {
+    for (; n + 2 < ne; n += 3) {
+      iter(std::integral_constant<int, 0>{}, n);
+      iter(std::integral_constant<int, 1>{}, n + 1);
+      iter(std::integral_constant<int, 2>{}, n + 2);
+    }
+    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
+    if (n + 1 < ne) iter(std::integral_constant<int, 1>{}, n + 1);
+  } else {
+    for (; n + 1 < ne; n += 2) {
+      iter(std::integral_constant<int, 0>{}, n);
+      iter(std::integral_constant<int, 1>{}, n + 1);
+    }
+    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
   }
-  if (n < ne) iter(std::integral_constant<int, 0>{}, n);
 
   a.epilogue(ti.b, ti.h, ti.split, qrow);
 }
@@ -750,6 +819,7 @@ static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int 
 
 struct Plan {
   int waves, block_m, num_m, num_n, splits, n_per_split;
+  int head_major;
   size_t o_part_bytes, lse_bytes, ws_bytes;
 };
 
@@ -778,6 +848,16 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
     if (w && (atoi(w) == 4 || atoi(w) == 8)) pl.waves = atoi(w);
   }
   pl.block_m = 32 * pl.waves;
+  // Workgroup order. Each XCD runs a contiguous range of tile ids and has its
+  // own L2. With few m-blocks per head, the mask tile (shared by all heads of
+  // a batch) is the stream worth sharing: heads fastest. Otherwise the K/V of
+  // a head (shared by its m-blocks) is: m-blocks fastest.
+  pl.head_major = ceil_div(p->seqlen_q, pl.block_m) <= 2 ? 1 : 0;
+  {
+    const char* o = getenv("MI355_FA_ORDER");   // tuning override: "h" or "m"
+    if (o && o[0] == 'h') pl.head_major = 1;
+    if (o && o[0] == 'm') pl.head_major = 0;
+  }
   pl.num_m = ceil_div(p->seqlen_q, pl.block_m);
   pl.n_per_split = (s > 1) ? ceil_div(pl.num_n, s) : pl.num_n;
   if (s > 1) {
@@ -948,6 +1028,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.num_splits = pl.splits; kp.n_per_split = pl.n_per_split;
   kp.total = (int)total;
   kp.scale = p->scale_softmax;
+  kp.head_major = pl.head_major;
   kp.mask_direct = (((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
                     (p->mask_row_stride & 7) == 0) ? 1 : 0;
 

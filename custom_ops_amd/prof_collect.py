@@ -1,0 +1,204 @@
+"""Collect the rocprofv3 evidence for one configuration and write text summaries.
+
+    python -m custom_ops_amd.prof_collect --config cfg2 --out gpurun_out/profiles
+
+Runs, each as its own rocprofv3 process under a hard time limit (this process
+never touches the GPU itself):
+  1. --kernel-trace --stats          per-kernel average duration
+  2. --pmc FETCH_SIZE                HBM read KiB per dispatch
+  3. --pmc WRITE_SIZE                HBM write KiB per dispatch
+  4. --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_MFMA GRBM_GUI_ACTIVE
+  5. --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS GRBM_GUI_ACTIVE
+The workload (custom_ops_amd.prof_workload) first runs y = 2·x over a 512 MiB
+fp32 buffer (5 dispatches of one elementwise kernel that reads and writes
+512 MiB each); its FETCH_SIZE / WRITE_SIZE against the known 512 MiB give the
+calibration factor applied to the attention kernel's counters.
+rocprofv3 reports GRBM_GUI_ACTIVE summed over the 8 XCDs; the per-XCD active
+cycles (GUI / 8) are the kernel's cycle count at the clock it ran at.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import shutil
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+COPY_MIB = 512
+
+PASSES = {
+    "trace": ["--kernel-trace", "--stats"],
+    "fetch": ["--pmc", "FETCH_SIZE"],
+    "write": ["--pmc", "WRITE_SIZE"],
+    "mfma": ["--pmc", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_MFMA",
+             "GRBM_GUI_ACTIVE"],
+    "lds": ["--pmc", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS",
+            "GRBM_GUI_ACTIVE"],
+}
+
+
+def workload_cmd(cfg: str, iters: int) -> list[str]:
+    return [sys.executable, "-m", "custom_ops_amd.prof_workload", "--config", cfg, "--iters",
+            str(iters), "--copy-mib", str(COPY_MIB)]
+
+
+def rocprof_cmd(name: str, outdir: str, cfg: str, iters: int) -> list[str]:
+    return ["rocprofv3", *PASSES[name], "--output-format", "csv", "-d", outdir, "--",
+            *workload_cmd(cfg, iters)]
+
+
+def run_pass(name: str, outdir: str, cfg: str, iters: int) -> str:
+    d = os.path.join(outdir, "raw", name)
+    shutil.rmtree(d, ignore_errors=True)
+    os.makedirs(d, exist_ok=True)
+    cmd = rocprof_cmd(name, d, cfg, iters)
+    env = dict(os.environ, TMPDIR="/tmp", PYTHONPATH=ROOT)
+    print("[prof]", " ".join(cmd), flush=True)
+    res = subprocess.run(["timeout", "-s", "KILL", "90", *cmd], cwd="/tmp", env=env,
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"pass {name} failed ({res.returncode}):\n{res.stdout[-2000:]}\n"
+                           f"{res.stderr[-2000:]}")
+    return d
+
+
+def rows(d: str, suffix: str) -> list[dict]:
+    out = []
+    for f in glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True):
+        with open(f, newline="") as fh:
+            out.extend(csv.DictReader(fh))
+    return out
+
+
+def is_attn(name: str) -> bool:
+    return "fa_fwd_kernel" in name
+
+
+def is_combine(name: str) -> bool:
+    return "fa_combine_kernel" in name
+
+
+def is_copy(name: str) -> bool:
+    return "MulFunctor" in name
+
+
+def counter_means(d: str, pred) -> dict[str, float]:
+    """Mean over matching dispatches of each counter (summed over its instances)."""
+    per = {}
+    for r in rows(d, "counter_collection.csv"):
+        if not pred(r["Kernel_Name"]):
+            continue
+        key = (r.get("Dispatch_Id") or r.get("Correlation_Id"), r["Counter_Name"])
+        per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    acc = {}
+    for (_, cname), v in per.items():
+        acc.setdefault(cname, []).append(v)
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--config", default="cfg2")
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "profiles"))
+    args = ap.parse_args()
+    os.makedirs(args.out, exist_ok=True)
+    sys.path.insert(0, ROOT)
+    from custom_ops_amd.workloads import CONFIGS
+    cfg = CONFIGS[args.config]
+
+    dirs = {p: run_pass(p, args.out, cfg.name, args.iters) for p in PASSES}
+
+    stats = rows(dirs["trace"], "kernel_stats.csv")
+    attn = [r for r in stats if is_attn(r["Name"])]
+    if not attn:
+        raise RuntimeError("no fa_fwd_kernel dispatch in the kernel trace")
+    avg_ns = float(attn[0]["AverageNs"])
+    comb = [r for r in stats if is_combine(r["Name"])]
+
+    fetch_copy = counter_means(dirs["fetch"], is_copy).get("FETCH_SIZE")
+    write_copy = counter_means(dirs["write"], is_copy).get("WRITE_SIZE")
+    fetch = counter_means(dirs["fetch"], is_attn)["FETCH_SIZE"]
+    write = counter_means(dirs["write"], is_attn)["WRITE_SIZE"]
+    kib = COPY_MIB * 1024
+    f_fac = kib / fetch_copy if fetch_copy else None
+    w_fac = kib / write_copy if write_copy else None
+    traffic = None
+    if f_fac and w_fac:
+        traffic = (fetch * f_fac + write * w_fac) * 1024
+    mf = counter_means(dirs["mfma"], is_attn)
+    ld = counter_means(dirs["lds"], is_attn)
+    simds, xcds = 256 * 4, 8
+    gui = mf["GRBM_GUI_ACTIVE"] / xcds
+    mfma_util = 100 * mf["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * simds)
+    mfma_flops = mf.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0) * 512
+    bank_conf = ld["SQ_LDS_BANK_CONFLICT"] / max(1.0, ld["SQ_LDS_IDX_ACTIVE"])
+
+    kname = attn[0]["Name"]
+    stem = f"fa_fwd_kernel_{cfg.name}"
+    mask_bytes = cfg.B * cfg.Sq * cfg.Sk * 2
+    summary = {
+        "config": cfg.name,
+        "kernel": kname,
+        "calls": int(attn[0]["Calls"]),
+        "avg_duration_us": avg_ns / 1e3,
+        "min_duration_us": float(attn[0]["MinNs"]) / 1e3,
+        "max_duration_us": float(attn[0]["MaxNs"]) / 1e3,
+        "combine_avg_us": float(comb[0]["AverageNs"]) / 1e3 if comb else None,
+        "achieved_tflops": cfg.flops / (avg_ns * 1e-9) / 1e12,
+        "pct_bf16_peak": 100 * cfg.flops / (avg_ns * 1e-9) / 1e12 / 2500.0,
+        "fetch_kib_raw": fetch, "write_kib_raw": write,
+        "copy_fetch_kib_raw": fetch_copy, "copy_write_kib_raw": write_copy,
+        "fetch_factor": f_fac, "write_factor": w_fac,
+        "hbm_bytes_per_launch": traffic,
+        "algorithmic_bytes_per_launch": cfg.algorithmic_bytes,
+        "hbm_gbps": traffic / (avg_ns * 1e-9) / 1e9 if traffic else None,
+        "mask_stream_gbps_algorithmic": mask_bytes / (avg_ns * 1e-9) / 1e9,
+        "mfma_busy_pct": mfma_util,
+        "active_cycles_per_xcd": gui,
+        "clock_ghz_under_counters": gui / (avg_ns * 1e-9) / 1e9,
+        "mfma_bf16_flops_counted": mfma_flops,
+        "mfma_insts": mf.get("SQ_INSTS_MFMA"),
+        "lds_bank_conflict_cycles": ld["SQ_LDS_BANK_CONFLICT"],
+        "lds_active_cycles": ld["SQ_LDS_IDX_ACTIVE"],
+        "lds_insts": ld["SQ_INSTS_LDS"],
+        "lds_bank_conflict_ratio": bank_conf,
+    }
+    with open(os.path.join(args.out, f"traffic_{stem}.json"), "w") as f:
+        json.dump({"config": cfg.name, "kernel": kname,
+                   "hbm_bytes_per_launch": traffic,
+                   "fetch_factor": f_fac, "write_factor": w_fac,
+                   "avg_duration_us": avg_ns / 1e3}, f, indent=1)
+    lines = [f"# rocprofv3 summary: fa_fwd_kernel on {cfg.name}", ""]
+    lines.append(f"workload: {cfg.name} B={cfg.B} H={cfg.H} Hk={cfg.Hk} Sq={cfg.Sq} Sk={cfg.Sk} "
+                 f"d={cfg.d} bf16 ({cfg.description}); {args.iters} launches after clock settle")
+    lines.append("")
+    lines.append("commands (run from the repository root; each pass is its own process):")
+    lines.append(f"  python -m custom_ops_amd.prof_collect --config {cfg.name} --iters {args.iters}")
+    for p in PASSES:
+        lines.append("  cd /tmp && TMPDIR=/tmp PYTHONPATH=<repo> " +
+                     " ".join(rocprof_cmd(p, f"<out>/raw/{p}", cfg.name, args.iters)))
+    lines.append("")
+    lines.append("kernel trace (--stats), all kernels:")
+    lines.append(f"  {'name':<70} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9}")
+    for r in stats:
+        lines.append(f"  {r['Name'][:70]:<70} {int(r['Calls']):>6} {float(r['AverageNs'])/1e3:>9.2f} "
+                     f"{float(r['MinNs'])/1e3:>9.2f} {float(r['MaxNs'])/1e3:>9.2f}")
+    lines.append("")
+    lines.append("derived:")
+    for k, v in summary.items():
+        if isinstance(v, float):
+            v = f"{v:.6g}"
+        lines.append(f"  {k:<34} {v}")
+    txt = "\n".join(lines) + "\n"
+    with open(os.path.join(args.out, f"{stem}.txt"), "w") as f:
+        f.write(txt)
+    print(txt, flush=True)
+
+
+if __name__ == "__main__":
+    main()
