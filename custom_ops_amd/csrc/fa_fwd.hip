@@ -60,7 +60,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBN = 64;       // keys per KV tile
+constexpr int kBN = 64;
+constexpr int kMaxLive = 2048;   // KV tiles one workgroup can list (Sk per split <= 131072)       // keys per KV tile
 constexpr int kMaxSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -575,7 +576,9 @@ __device__ __forceinline__ uint16_t* stage_buf(uint16_t* b0, uint16_t* b1, uint1
 //   wait until tile n's loads have landed (tiles n+1 .. n+NS-2 may still be in
 //   flight) + barrier; issue K, V, mask of tile n+NS-1 into the stage freed by
 //   tile n-1; Sᵀ(n) = K(n)·Qᵀ; + mask(n); softmax(n) fused with
-//   Oᵀ += Vᵀ(n)·Pᵀ(n). One barrier per tile.
+//   Oᵀ += Vᵀ(n)·Pᵀ(n). One barrier per tile. (Skipping tiles whose mask block
+//   is all -inf measured slower on masks without such blocks: the tile's DMA,
+//   wait and barrier remain, and the test costs LDS reads and VALU.)
 // Unaligned mask rows go through registers one tile ahead instead (loaded
 // before the DMAs so waiting for them does not wait for the DMAs).
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
@@ -610,63 +613,69 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
     if constexpr (NS == 3) reinterpret_cast<u32x4*>(sV2)[i] = u32x4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
-  // prologue: tiles nb .. nb+NS-2
-  if (nb < ne) {
-    a.issue_m(nb, sM0);
-    a.issue_k(nb, sK0);
-    a.issue_v(nb, sV0);
+  const int cnt = ne - nb;
+  auto tile = [&](int i) -> int { return nb + i; };   // visit order
+  // prologue: tiles 0 .. NS-2 of the visit order
+  if (cnt > 0) {
+    const int t0 = tile(0);
+    a.issue_m(t0, sM0);
+    a.issue_k(t0, sK0);
+    a.issue_v(t0, sV0);
   }
   if constexpr (NS == 3) {
-    if (nb + 1 < ne) {
-      if constexpr (MDIRECT) a.issue_m(nb + 1, sM1);
-      a.issue_k(nb + 1, sK1);
-      a.issue_v(nb + 1, sV1);
+    if (1 < cnt) {
+      const int t1 = tile(1);
+      if constexpr (MDIRECT) a.issue_m(t1, sM1);
+      a.issue_k(t1, sK1);
+      a.issue_v(t1, sV1);
     }
   }
   a.load_q(qrow, rq);
-  if (nb < ne) a.commit_m(sM0);
+  if (cnt > 0) a.commit_m(sM0);
 
-  auto iter = [&](auto stc, int n) {
+  auto iter = [&](auto stc, int i) {
     constexpr int ST = decltype(stc)::value;
-    constexpr int NX = (ST + NS - 1) % NS;   // receives tile n+NS-1
-    constexpr int N1 = (ST + 1) % NS;        // holds tile n+1
+    constexpr int NX = (ST + NS - 1) % NS;   // receives visit i+NS-1
+    constexpr int N1 = (ST + 1) % NS;        // holds visit i+1
+    const int n = tile(i);
     if constexpr (NS == 3) {
-      if (n + 1 < ne) wait_vmcnt<kL>();
+      if (i + 1 < cnt) wait_vmcnt<kL>();
       else wait_vmcnt<0>();
     } else {
       wait_vmcnt<0>();
     }
     __syncthreads();
     if constexpr (!MDIRECT) {
-      if (n + 1 < ne) a.issue_m(n + 1, nullptr);   // into registers
+      if (i + 1 < cnt) a.issue_m(tile(i + 1), nullptr);   // into registers
     }
-    if (n + NS - 1 < ne) {
-      if constexpr (MDIRECT) a.issue_m(n + NS - 1, stage_buf<NX>(sM0, sM1, sM2));
-      a.issue_k(n + NS - 1, stage_buf<NX>(sK0, sK1, sK2));
-      a.issue_v(n + NS - 1, stage_buf<NX>(sV0, sV1, sV2));
+    if (i + NS - 1 < cnt) {
+      const int nx = tile(i + NS - 1);
+      if constexpr (MDIRECT) a.issue_m(nx, stage_buf<NX>(sM0, sM1, sM2));
+      a.issue_k(nx, stage_buf<NX>(sK0, sK1, sK2));
+      a.issue_v(nx, stage_buf<NX>(sV0, sV1, sV2));
     }
     a.qk(stage_buf<ST>(sK0, sK1, sK2));
     a.add_mask(stage_buf<ST>(sM0, sM1, sM2), n);
     a.softmax_pv(stage_buf<ST>(sV0, sV1, sV2));
     if constexpr (!MDIRECT) {
-      if (n + 1 < ne) a.commit_m(stage_buf<N1>(sM0, sM1, sM2));
+      if (i + 1 < cnt) a.commit_m(stage_buf<N1>(sM0, sM1, sM2));
     }
   };
-  int n = nb;
+  int i = 0;
   if constexpr (NS == 3) {
-    for (; n + 2 < ne; n += 3) {
-      iter(std::integral_constant<int, 0>{}, n);
-      iter(std::integral_constant<int, 1>{}, n + 1);
-      iter(std::integral_constant<int, 2>{}, n + 2);
+    for (; i + 2 < cnt; i += 3) {
+      iter(std::integral_constant<int, 0>{}, i);
+      iter(std::integral_constant<int, 1>{}, i + 1);
+      iter(std::integral_constant<int, 2>{}, i + 2);
     }
-    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
-    if (n + 1 < ne) iter(std::integral_constant<int, 1>{}, n + 1);
+    if (i < cnt) iter(std::integral_constant<int, 0>{}, i);
+    if (i + 1 < cnt) iter(std::integral_constant<int, 1>{}, i + 1);
   } else {
-    for (; n + 1 < ne; n += 2) {
-      iter(std::integral_constant<int, 0>{}, n);
-      iter(std::integral_constant<int, 1>{}, n + 1);
+    for (; i + 1 < cnt; i += 2) {
+      iter(std::integral_constant<int, 0>{}, i);
+      iter(std::integral_constant<int, 1>{}, i + 1);
     }
-    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
+    if (i < cnt) iter(std::integral_constant<int, 0>{}, i);
   }
 
   a.epilogue(ti.b, ti.h, ti.split, qrow);
@@ -789,7 +798,11 @@ static int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // fa_mask_sm89_num_splits, csrc/fa/fa_fwd_launch.h:137-170): split only when
 // the grid of row tiles under-fills the chip; K = relative cost of one KV tile
 // in the main kernel, P = per-split cost of the partial write + combine.
-static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int cus) {
+// slots = workgroups resident per CU: the reference's kernel fits 2 per SM
+// (cap_fill = 2·SMs / m-blocks, which the exported mi355_fa_cost_model_splits
+// keeps); the 4-wave kernel here holds 96 KiB of LDS, so 1 per CU.
+static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int cus,
+                             int slots = 2) {
   if (cus <= 0) cus = 1;
   if (total_mblocks <= 0 || nb <= 0) return 1;
   if (total_mblocks >= 0.8f * cus) return 1;
@@ -798,7 +811,7 @@ static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int 
   const int combine_units = total_mblocks * (block_m / 32) * (d / 32);
   const float P = fmaxf(0.35f, (float)combine_units / (float)cus);
   const float s_star = sqrtf((float)nb * K / P);
-  const int cap_fill = (2 * cus) / total_mblocks > 1 ? (2 * cus) / total_mblocks : 1;
+  const int cap_fill = (slots * cus) / total_mblocks > 1 ? (slots * cus) / total_mblocks : 1;
   int hi = (int)s_star + 8;
   if (hi > kMaxSplits) hi = kMaxSplits;
   if (hi > nb) hi = nb;
@@ -823,9 +836,9 @@ struct Plan {
   size_t o_part_bytes, lse_bytes, ws_bytes;
 };
 
-// Tile plan. BM = 256 rows (8 waves) when that grid fills the chip; otherwise
-// BM = 128 (4 waves), with split-KV chosen by the cost model when even that
-// grid leaves CUs idle.
+// Tile plan. BM = 256 rows (8 waves) when that grid fills the chip, alone or
+// with 2..4 KV splits; otherwise BM = 128 (4 waves), with split-KV chosen by
+// the cost model when even that grid leaves CUs idle.
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
   pl.num_n = ceil_div(p->seqlen_k, kBN);
@@ -837,12 +850,21 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   }
   const int m256 = ceil_div(p->seqlen_q, 256), m128 = ceil_div(p->seqlen_q, 128);
   const bool big = (float)bh * m256 >= 0.8f * cus;
-  if (s <= 0) s = big ? 1 : cost_model_splits(bh * m128, pl.num_n, 128, p->d, cus);
+  // 8 waves (BM = 256, two waves per SIMD) run far better than 4 (one wave
+  // per SIMD), so a grid of 256-row tiles that is short of the chip is first
+  // topped up with 2..4 KV splits, provided the tiles are mostly real rows and
+  // every split keeps >= 8 KV tiles.
+  int fill8 = 0;
+  if (!big && p->seqlen_q >= 192 * m256) {
+    for (int c = 2; c <= 4 && !fill8; ++c)
+      if ((float)bh * m256 * c >= 0.8f * cus && pl.num_n >= 8 * c) fill8 = c;
+  }
+  if (s <= 0) s = big ? 1 : fill8 ? fill8 : cost_model_splits(bh * m128, pl.num_n, 128, p->d, cus, 1);
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > pl.num_n) s = pl.num_n;
   if (s < 1) s = 1;
   pl.splits = s;
-  pl.waves = (s == 1 && big) ? 8 : 4;
+  pl.waves = ((s == 1 && big) || (fill8 && s == fill8)) ? 8 : 4;
   {   // tuning override of the workgroup size (4 or 8 waves)
     const char* w = getenv("MI355_FA_WAVES");
     if (w && (atoi(w) == 4 || atoi(w) == 8)) pl.waves = atoi(w);
@@ -864,8 +886,8 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
     const size_t rows = (size_t)s * p->b * p->h * p->seqlen_q;
     pl.o_part_bytes = (rows * p->d * sizeof(float) + 255) & ~(size_t)255;
     pl.lse_bytes = (rows * sizeof(float) + 255) & ~(size_t)255;
-    pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes;
   }
+  pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes;
   return pl;
 }
 
@@ -1007,7 +1029,8 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   }
   const bool split = pl.splits > 1;
   if (split && (!p->workspace || p->workspace_bytes < pl.ws_bytes)) {
-    set_err(err, errlen, "split-KV needs %zu workspace bytes, got %zu", pl.ws_bytes, p->workspace_bytes);
+    set_err(err, errlen, "split-KV needs %zu workspace bytes, got %zu", pl.ws_bytes,
+            p->workspace_bytes);
     return MI355_FA_EWORKSPACE;
   }
 

@@ -197,6 +197,48 @@ def test_workgroup_variants(ops, gpu, monkeypatch, waves, splits, d, dtype, sk, 
     assert torch.all(out[1, :, 17, :] == 0)
 
 
+def _skip_mask(kind, b, sq, sk, g):
+    m = torch.zeros(b, 1, sq, sk)
+    rows = torch.arange(sq).view(-1, 1)
+    cols = torch.arange(sk).view(1, -1)
+    if kind == "causal":              # bottom-right aligned causal
+        m.masked_fill_(cols > rows + (sk - sq), float("-inf"))
+    elif kind == "window":            # 256-key sliding window, bottom-right aligned
+        off = rows + (sk - sq)
+        m.masked_fill_((cols > off) | (cols < off - 255), float("-inf"))
+    elif kind == "dead_stripes":      # whole 64-key tiles dead, then a lone live key
+        dead = ((cols // 64) % 3 == 1) | ((cols // 64) % 5 == 2)
+        m.masked_fill_(dead, float("-inf"))
+        m[..., 64 * 4 + 17] = 0.0     # tile 4 is live again through one column
+    elif kind == "pad_rows_cols":     # batch-1 keys >= sk-300 blocked, rows >= 400 see nothing
+        m[1, :, :, sk - 300:] = float("-inf")
+        m[:, :, 400:, :] = float("-inf")
+    m.masked_fill_(torch.rand(b, 1, sq, sk, generator=g) < 0.05, float("-inf"))
+    return m
+
+
+@pytest.mark.parametrize("kind", ["causal", "window", "dead_stripes", "pad_rows_cols"])
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_dead_mask_blocks(ops, gpu, monkeypatch, kind, waves, splits):
+    """Masks with whole 32-row x 64-key blocks at -inf (a wave skips the QK /
+    softmax / PV work of such a tile): results match the fp32 reference, and
+    rows that see no key are exactly 0."""
+    from custom_ops_amd import mha_fwd_with_mask
+    monkeypatch.setenv("MI355_FA_WAVES", str(waves))
+    g = torch.Generator().manual_seed(7)
+    b, h, hk, sq, sk, d = 2, 4, 2, 700, 1500, 128
+    q = _rand((b, h, sq, d), g).to(torch.bfloat16).to(gpu)
+    k = _rand((b, hk, sk, d), g).to(torch.bfloat16).to(gpu)
+    v = _rand((b, hk, sk, d), g).to(torch.bfloat16).to(gpu)
+    m = _skip_mask(kind, b, sq, sk, g).to(torch.bfloat16).to(gpu)
+    out = mha_fwd_with_mask(q, k, v, m, num_splits=splits)
+    torch.cuda.synchronize()
+    assert_close(out, ref_attn_torch(q, k, v, m), f"dead blocks {kind} w{waves} s{splits}")
+    dead_rows = torch.isinf(m).all(-1).squeeze(1)          # [b, sq]
+    assert torch.all(out.permute(0, 2, 1, 3)[dead_rows] == 0)
+
+
 def test_all_masked_everything_split(ops, gpu):
     q, k, v, m = make_case(1, 2, 2, 64, 4096, 128, "zero", torch.bfloat16)
     m = torch.full_like(m, float("-inf"))
