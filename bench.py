@@ -10,10 +10,12 @@ inputs resident in HBM. Prints ONE JSON line:
                  FLOP count, benchmark/benchmark_fa.py:135-137) over K steps
   roofline     = dominant kernel (fa_fwd_kernel) achieved TFLOP/s vs the
                  MI355X dense bf16 MFMA peak, from HIP events on the launch stream
-  configs      = per-config latency (µs) measured the reference's way (median
-                 of N after warmup, >= 512 MB written between iterations to
-                 flush L2 + MALL; benchmark/benchmark_fa.py:115-132), and
-                 "us_hot": back-to-back launches at settled clocks
+  configs      = per-config latency (µs): "us" the reference's way (median of
+                 N after warmup, a 256 MB buffer zeroed before each iteration,
+                 benchmark/benchmark_fa.py:115-132); "us_cold" with a 512 MB
+                 buffer zeroed AND read back (cold, clean L2 + MALL: no dirty
+                 flush lines to write back inside the timed call); "us_hot"
+                 back-to-back launches at settled clocks
   cpu_baseline = PyTorch fp32 math attention on this host's cores over a
                  time-bounded sample of (b, h) heads of the same workload.
 """
@@ -39,14 +41,19 @@ def parse():
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--settle-s", type=float, default=0.5,
                     help="untimed back-to-back steps before warmup, in seconds (clock ramp)")
-    ap.add_argument("--ref-iters", type=int, default=30)
+    ap.add_argument("--ref-iters", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     return ap.parse_args()
 
 
-def ref_method_us(fn, warmup, iters, flush):
+def ref_method_us(fn, warmup, iters, flush, reread=None):
+    """The reference's timing (benchmark/benchmark_fa.py:115-132): per iteration
+    zero a flush buffer, then time one call with events; no host sync between
+    iterations; median. With ``reread`` the flush buffer is also read back, so
+    the timed call starts with cold but clean caches (no dirty lines left by
+    the flush to write back)."""
     import torch
     for _ in range(warmup):
         fn()
@@ -55,6 +62,8 @@ def ref_method_us(fn, warmup, iters, flush):
     en = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     for i in range(iters):
         flush.zero_()
+        if reread is not None:
+            torch.amax(flush, dim=0, out=reread)
         st[i].record()
         fn()
         en[i].record()
@@ -202,7 +211,9 @@ def main():
     }
 
     if not args.no_configs:
-        flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+        flush_ref = torch.empty(256 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+        flush_big = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+        reread = torch.empty((), dtype=torch.int32, device=dev)
         confs = {}
         for name in ("cfg2", "cfg3", "cfg4", "cfg5"):
             c = CONFIGS[name]
@@ -211,20 +222,19 @@ def main():
             else:
                 tq, tk, tv, tm = (t.to(dev) for t in make_inputs(c))
             fnc = lambda: ops.mha_fwd_with_mask(tq, tk, tv, tm)  # noqa: E731
-            us = ref_method_us(fnc, 5, args.ref_iters, flush)
+            us = ref_method_us(fnc, 10, args.ref_iters, flush_ref)
+            us_cold = ref_method_us(fnc, 5, args.ref_iters, flush_big, reread)
             us_hot = hot_us(fnc)
-            tf = c.flops / (us * 1e-6) / 1e12
-            tf_hot = c.flops / (us_hot * 1e-6) / 1e12
-            confs[name] = {"us": round(us, 2), "tflops": round(tf, 2),
-                           "pct_bf16_peak": round(100 * tf / MI355X_BF16_DENSE_TFLOPS, 2),
-                           "hbm_gbps_algorithmic": round(c.algorithmic_bytes / (us * 1e-6) / 1e9,
-                                                         1),
-                           "us_hot": round(us_hot, 2),
-                           "pct_bf16_peak_hot": round(100 * tf_hot / MI355X_BF16_DENSE_TFLOPS, 2),
-                           "hbm_gbps_algorithmic_hot": round(
-                               c.algorithmic_bytes / (us_hot * 1e-6) / 1e9, 1)}
+            confs[name] = {"us": round(us, 2)}
+            for key, t in (("", us), ("_cold", us_cold), ("_hot", us_hot)):
+                tf = c.flops / (t * 1e-6) / 1e12
+                confs[name]["us" + key] = round(t, 2)
+                confs[name]["tflops" + key] = round(tf, 2)
+                confs[name]["pct_bf16_peak" + key] = round(100 * tf / MI355X_BF16_DENSE_TFLOPS, 2)
+                confs[name]["hbm_gbps_algorithmic" + key] = round(
+                    c.algorithmic_bytes / (t * 1e-6) / 1e9, 1)
             del tq, tk, tv, tm
-        del flush
+        del flush_ref, flush_big
         result["configs"] = confs
 
     if not args.no_cpu:
