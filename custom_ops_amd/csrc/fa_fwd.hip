@@ -118,7 +118,7 @@ struct KParams {
   const uint16_t* v;
   const uint16_t* mask;
   uint16_t* o;
-  float* o_part;   // [splits][B*H][Sq][D] fp32 (split path)
+  uint16_t* o_part; // [splits][B*H][Sq][D] input dtype (split path)
   float* lse_part; // [splits][B*H][Sq]    fp32, natural log
 
   int64_t q_bs, q_hs;
@@ -280,6 +280,7 @@ struct Attn {
   typedef Geo<D, WAVES> G;
   static constexpr int KD = D / 16;
   static constexpr int DB = D / 32;
+  static constexpr int NKB = 2;   // 32-key blocks per tile
 
   const KParams& p;
   int tid, lane, wave, l32, g;
@@ -295,9 +296,13 @@ struct Attn {
   uint32_t m_rd[4];
   V8 qreg[KD];
   f32x16 oacc[DB];
-  f32x16 s[2];
+  f32x16 s[NKB];
   u32x4 mreg[MDIRECT ? 1 : G::kMWaveLoads];
+  // Scores live in the reference's unscaled domain u = q·k + mask·(1/scale)
+  // (csrc/fa/sm89/fa_fwd_kernel.h:286-310); m_run is a max of u, and
+  // exp(x - max) = exp2(u·c2 - m_run·c2) with c2 = scale·log2(e) (softmax.h:87).
   float m_run, mlog2, l_run;
+  float c2, inv_scale, slack_u;
 
   __device__ __forceinline__ Attn(const KParams& p_) : p(p_) {}
 
@@ -347,7 +352,7 @@ struct Attn {
     }
     const int mr = wave * 32 + l32;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2 * NKB; ++i) {
       const int u = (i / 2) * 4 + 2 * g + (i % 2);
       m_rd[i] = (uint32_t)(mr * kBN + ((u ^ mask_swz(mr)) * 8)) * 2u;
     }
@@ -355,6 +360,9 @@ struct Attn {
     for (int i = 0; i < DB; ++i) oacc[i] = f32x16{};
     m_run = -INFINITY;
     mlog2 = 0.f;
+    c2 = p.scale * kLog2e;
+    inv_scale = 1.f / p.scale;
+    slack_u = kRescaleSlack / p.scale;
     l_run = 0.f;
   }
 
@@ -424,15 +432,32 @@ struct Attn {
       bload16_lds(r, sV + (i * G::kWaves + wave) * 64 * 8, v_off[i]);
   }
 
-  // Sᵀ = K·Qᵀ; operands stream through a window of kWin LDS reads in flight.
+  // u = mask·(1/scale) + K·Qᵀ: the widened, pre-scaled mask tile initialises the
+  // accumulators, so no pass over the scores is needed between the two GEMMs
+  // (the mask work overlaps the MFMAs of the other key block). K operands
+  // stream through a window of kWin LDS reads in flight.
   static constexpr int kWin = 2;
-  __device__ __forceinline__ void qk(const uint16_t* sK) {
-    s[0] = f32x16{};
-    s[1] = f32x16{};
+  typedef f32x16 Scores[NKB];
+
+  __device__ __forceinline__ void mask_init(const uint16_t* sM) { mask_init(sM, s); }
+  __device__ __forceinline__ void mask_init(const uint16_t* sM, Scores& sc) {
+    const uint8_t* mb = reinterpret_cast<const uint8_t*>(sM);
+#pragma unroll
+    for (int b = 0; b < NKB; ++b) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * b]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * b + 1]);
+      const f32x16 mk = mask_to_f32<BF16>(lo, hi);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[b][i] = mk[i] * inv_scale;
+    }
+  }
+
+  __device__ __forceinline__ void qk(const uint16_t* sK) { qk(sK, s); }
+  __device__ __forceinline__ void qk(const uint16_t* sK, Scores& sc) {
     const uint8_t* kb8 = reinterpret_cast<const uint8_t*>(sK);
-    constexpr int N = 2 * KD;   // step i: kd = i / 2, kb = i % 2
+    constexpr int N = NKB * KD;   // step i: local block i / KD, kd = i % KD
     auto rd = [&](int i) {
-      return bitcast<V8>(*reinterpret_cast<const u32x4*>(kb8 + (i % 2) * 32 * D * 2 + k_rd[i / 2]));
+      return bitcast<V8>(*reinterpret_cast<const u32x4*>(kb8 + (i / KD) * 32 * D * 2 + k_rd[i % KD]));
     };
     V8 win[kWin];
 #pragma unroll
@@ -441,28 +466,20 @@ struct Attn {
     for (int i = 0; i < N; ++i) {
       const V8 a = win[i % kWin];
       if (i + kWin < N) win[i % kWin] = rd(i + kWin);
-      s[i % 2] = Elt<BF16>::mfma(a, qreg[i / 2], s[i % 2]);
+      sc[i / KD] = Elt<BF16>::mfma(a, qreg[i % KD], sc[i / KD]);
     }
   }
 
-  // scores of tile n: S·scale + mask, keys past Sk → -inf
-  __device__ __forceinline__ void add_mask(const uint16_t* sM, int n) {
-    const uint8_t* mb = reinterpret_cast<const uint8_t*>(sM);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * kb]);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * kb + 1]);
-      const f32x16 mk = mask_to_f32<BF16>(lo, hi);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[kb][i] = __builtin_fmaf(s[kb][i], p.scale, mk[i]);
-    }
+  // keys past Sk → -inf (only the last tile of a head reaches past Sk)
+  __device__ __forceinline__ void apply_tail(int n) { apply_tail(n, s); }
+  __device__ __forceinline__ void apply_tail(int n, Scores& sc) {
     if ((n + 1) * kBN > p.sk) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int b = 0; b < NKB; ++b)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int key = n * kBN + kb * 32 + g * 16 + i;
-          s[kb][i] = (key < p.sk) ? s[kb][i] : -INFINITY;
+          const int key = n * kBN + b * 32 + g * 16 + i;
+          sc[b][i] = (key < p.sk) ? sc[b][i] : -INFINITY;
         }
     }
   }
@@ -470,25 +487,36 @@ struct Attn {
   // softmax of tile n and Oᵀ += Vᵀ·Pᵀ, the exponentials of each key step one
   // step ahead of its MFMAs
   __device__ __forceinline__ void softmax_pv(const uint16_t* sVt) {
+    rescale(s);
+    exp_pv(sVt, s);
+  }
+
+  // row max of a tile's scores; moves the running max (and rescales O, l)
+  // only when it grew by more than the slack
+  __device__ __forceinline__ void rescale(const Scores& sc) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int b = 0; b < NKB; ++b)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[b][i]);
     mx = xhalf_max(mx);
-    const bool need = mx > m_run + kRescaleSlack;
+    const bool need = mx > m_run + slack_u;
     if (__builtin_amdgcn_ballot_w64(need)) {
       // lanes that keep their max scale by exactly 1 (also avoids -inf - -inf)
-      const float alpha = need ? __builtin_amdgcn_exp2f((m_run - mx) * kLog2e) : 1.f;
+      const float alpha = need ? __builtin_amdgcn_exp2f((m_run - mx) * c2) : 1.f;
       m_run = need ? mx : m_run;
-      mlog2 = (m_run == -INFINITY) ? 0.f : m_run * kLog2e;
+      mlog2 = (m_run == -INFINITY) ? 0.f : m_run * c2;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
     }
-    // PV operands (step i: key step j = i / DB, d block db = i % DB) stream
-    // through a window of kWin LDS reads in flight.
-    constexpr int N = 4 * DB;
+  }
+
+  // P = exp2(u·c2 − m_run·c2) rounded to the input dtype; l += Σ P; Oᵀ += Vᵀ·Pᵀ
+  __device__ __forceinline__ void exp_pv(const uint16_t* sVt, const Scores& sc) {
+    // PV operands (step i: local key step j = i / DB of 8 keys, d block
+    // db = i % DB) stream through a window of kWin LDS reads in flight.
+    constexpr int N = 2 * NKB * DB;
     const uint8_t* vb = reinterpret_cast<const uint8_t*>(sVt);
     auto rd = [&](int i) {
       const int j = i / DB, db = i % DB;
@@ -509,7 +537,7 @@ struct Attn {
         f32x8 pf;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          pf[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j / 2][(j % 2) * 8 + e], kLog2e, -mlog2));
+          pf[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j / 2][(j % 2) * 8 + e], c2, -mlog2));
         pb = __builtin_convertvector(pf, V8);
         l_run = psum8<BF16>(pb, l_run);
       }
@@ -546,7 +574,9 @@ struct Attn {
       const int64_t bh = (int64_t)b * p.h + h;
       const int64_t slab = (int64_t)p.b * p.h * p.sq;
       const int64_t prow = (int64_t)split * slab + bh * p.sq + qrow;
-      float* op = p.o_part + prow * D;
+      // partial O normalised by the split's own l, rounded to the input
+      // dtype as the reference stores it (fa_fwd_launch.h:289-297)
+      uint16_t* op = p.o_part + prow * D;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
@@ -554,12 +584,17 @@ struct Attn {
           f32x4 v4;
 #pragma unroll
           for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
-          *reinterpret_cast<f32x4*>(op + db * 32 + q4 * 8 + g * 4) = v4;
+          typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+          typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+          u32x2 packed;
+          if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
+          else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
+          *reinterpret_cast<u32x2*>(op + db * 32 + q4 * 8 + g * 4) = packed;
         }
       }
       if (g == 0)
         p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY
-                                                 : m_run + __builtin_amdgcn_logf(l) * 0.69314718f;
+                                                 : m_run * p.scale + __builtin_amdgcn_logf(l) * 0.69314718f;
     }
   }
 };
@@ -654,8 +689,9 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
       a.issue_k(nx, stage_buf<NX>(sK0, sK1, sK2));
       a.issue_v(nx, stage_buf<NX>(sV0, sV1, sV2));
     }
+    a.mask_init(stage_buf<ST>(sM0, sM1, sM2));
     a.qk(stage_buf<ST>(sK0, sK1, sK2));
-    a.add_mask(stage_buf<ST>(sM0, sM1, sM2), n);
+    a.apply_tail(n);
     a.softmax_pv(stage_buf<ST>(sV0, sV1, sV2));
     if constexpr (!MDIRECT) {
       if (i + 1 < cnt) a.commit_m(stage_buf<N1>(sM0, sM1, sM2));
@@ -683,7 +719,7 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
 
 // ── split-KV combine ────────────────────────────────────────────────────────
 struct CParams {
-  const float* o_part;
+  const uint16_t* o_part;
   const float* lse_part;
   uint16_t* o;
   int64_t o_bs, o_hs, o_rs;
@@ -691,13 +727,15 @@ struct CParams {
   int64_t rows;  // B*H*Sq
 };
 
-// Workgroup = kRows rows × D columns; thread = 4 consecutive d-values of a row.
-// Phase 1 stages the rows' LSEs in LDS and turns them into weights
-// w_s = exp(lse_s − max) / Σ (all-(-inf) row → all weights 0 → output 0);
-// phase 2 accumulates Σ w_s·O_s with independent, unrolled loads.
+// Workgroup = kRows rows × D columns; thread = 8 consecutive d-values of a row
+// (one 16-byte load per split). Phase 1 stages the rows' LSEs in LDS and turns
+// them into weights w_s = exp(lse_s − max) / Σ (all-(-inf) row → all weights
+// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 8 splits'
+// loads in flight.
 template <int D, bool BF16>
 __global__ __launch_bounds__(256) void fa_combine_kernel(const CParams p) {
-  constexpr int kTPR = D / 4;              // threads per row
+  typedef typename Elt<BF16>::v8 V8;
+  constexpr int kTPR = D / 8;              // threads per row
   constexpr int kRows = 256 / kTPR;        // rows per workgroup
   __shared__ float sw[kMaxSplits * kRows];
   const int tid = threadIdx.x;
@@ -725,28 +763,26 @@ __global__ __launch_bounds__(256) void fa_combine_kernel(const CParams p) {
   }
   __syncthreads();
   const int r = tid / kTPR;
-  const int c4 = tid % kTPR;
+  const int c8 = tid % kTPR;
   const int64_t row = row0 + r;
   if (row >= p.rows) return;
-  const float* src = p.o_part + row * D + c4 * 4;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int s = 0;
-  for (; s + 4 <= S; s += 4) {
-    f32x4 v[4];
+  const uint16_t* src = p.o_part + row * D + c8 * 8;
+  f32x8 acc = {};
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    u32x4 raw[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(src + (s + u) * slab * D);
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) raw[u] = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + u) * slab * D);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc += sw[(s + u) * kRows + r] * v[u];
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S)
+        acc += sw[(s0 + u) * kRows + r] * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
   }
-  for (; s < S; ++s) acc += sw[s * kRows + r] * *reinterpret_cast<const f32x4*>(src + s * slab * D);
   const int64_t bh = row / p.sq;
   const int m = (int)(row % p.sq);
   const int b = (int)(bh / p.h), h = (int)(bh % p.h);
-  uint16_t* dst = p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs + (int64_t)m * p.o_rs + c4 * 4;
-  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-  typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
-  if constexpr (BF16) *reinterpret_cast<u32x2*>(dst) = bitcast<u32x2>(__builtin_convertvector(acc, bf16x4));
-  else *reinterpret_cast<u32x2*>(dst) = bitcast<u32x2>(__builtin_convertvector(acc, f16x4));
+  uint16_t* dst = p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs + (int64_t)m * p.o_rs + c8 * 8;
+  *reinterpret_cast<u32x4*>(dst) = bitcast<u32x4>(__builtin_convertvector(acc, V8));
 }
 
 // ════════════════════════════════════════════════════════════════════════════
@@ -884,7 +920,7 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   pl.n_per_split = (s > 1) ? ceil_div(pl.num_n, s) : pl.num_n;
   if (s > 1) {
     const size_t rows = (size_t)s * p->b * p->h * p->seqlen_q;
-    pl.o_part_bytes = (rows * p->d * sizeof(float) + 255) & ~(size_t)255;
+    pl.o_part_bytes = (rows * p->d * sizeof(uint16_t) + 255) & ~(size_t)255;
     pl.lse_bytes = (rows * sizeof(float) + 255) & ~(size_t)255;
   }
   pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes;
@@ -962,7 +998,7 @@ static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, h
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
   hipError_t e = launch_variant<D, BF16, true>(kp, pl, st);
   if (e != hipSuccess) return e;
-  constexpr int kRows = 256 / (D / 4);
+  constexpr int kRows = 256 / (D / 8);
   const int64_t blocks = (cp.rows + kRows - 1) / kRows;
   hipLaunchKernelGGL((fa_combine_kernel<D, BF16>), dim3((unsigned)blocks), dim3(256), 0, st, cp);
   return hipGetLastError();
@@ -1057,7 +1093,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
 
   CParams cp{};
   if (split) {
-    kp.o_part = (float*)p->workspace;
+    kp.o_part = (uint16_t*)p->workspace;
     kp.lse_part = (float*)((char*)p->workspace + pl.o_part_bytes);
     cp.o_part = kp.o_part;
     cp.lse_part = kp.lse_part;

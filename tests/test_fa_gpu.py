@@ -181,7 +181,7 @@ def test_split_invariance(ops, gpu, splits):
     assert torch.all(out[:, :, 5, :] == 0)
 
 
-@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("waves", ["4", "8"])
 @pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp16"])
@@ -190,7 +190,7 @@ def test_workgroup_variants(ops, gpu, monkeypatch, waves, splits, d, dtype, sk, 
     """Both workgroup sizes (4 waves / BM 128, 8 waves / BM 256), forced through
     the single-pass and split-KV epilogues, with 16-byte-aligned mask rows (LDS
     DMA) and unaligned ones (register path)."""
-    monkeypatch.setenv("MI355_FA_WAVES", str(waves))
+    monkeypatch.setenv("MI355_FA_WAVES", waves)
     case = make_case(2, 4, 2, 300, sk, d, "inf_random", dtype, extra_cols=extra_cols)
     case[3][1, :, 17, :] = float("-inf")
     out, _ = run(ops, case, gpu, f"w{waves} s{splits} d{d} sk{sk}", num_splits=splits)
@@ -218,14 +218,14 @@ def _skip_mask(kind, b, sq, sk, g):
 
 
 @pytest.mark.parametrize("kind", ["causal", "window", "dead_stripes", "pad_rows_cols"])
-@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("waves", ["4", "8"])
 @pytest.mark.parametrize("splits", [1, 3])
 def test_dead_mask_blocks(ops, gpu, monkeypatch, kind, waves, splits):
     """Masks with whole 32-row x 64-key blocks at -inf (a wave skips the QK /
     softmax / PV work of such a tile): results match the fp32 reference, and
     rows that see no key are exactly 0."""
     from custom_ops_amd import mha_fwd_with_mask
-    monkeypatch.setenv("MI355_FA_WAVES", str(waves))
+    monkeypatch.setenv("MI355_FA_WAVES", waves)
     g = torch.Generator().manual_seed(7)
     b, h, hk, sq, sk, d = 2, 4, 2, 700, 1500, 128
     q = _rand((b, h, sq, d), g).to(torch.bfloat16).to(gpu)

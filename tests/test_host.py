@@ -111,7 +111,7 @@ def test_cost_model_and_workspace(lib):
     p = _params(num_splits=200, seqlen_k=64 * 100, mask_seqlen_k=64 * 100)
     assert _lib.num_splits(p) == 64
     rows = 64 * 1 * 4 * 128
-    assert _lib.workspace_bytes(p) >= rows * 128 * 4 + rows * 4
+    assert _lib.workspace_bytes(p) >= rows * 128 * 2 + rows * 4   # 16-bit O partials + fp32 LSE
     p = _params(num_splits=1)
     assert _lib.num_splits(p) == 1 and _lib.workspace_bytes(p) == 0
 
