@@ -687,10 +687,10 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
       const int nx = tile(i + NS - 1);
       if constexpr (MDIRECT) a.issue_m(nx, stage_buf<NX>(sM0, sM1, sM2));
       a.issue_k(nx, stage_buf<NX>(sK0, sK1, sK2));
-      a.issue_v(nx, stage_buf<NX>(sV0, sV1, sV2));
     }
     a.mask_init(stage_buf<ST>(sM0, sM1, sM2));
     a.qk(stage_buf<ST>(sK0, sK1, sK2));
+    if (i + NS - 1 < cnt) a.issue_v(tile(i + NS - 1), stage_buf<NX>(sV0, sV1, sV2));
     a.apply_tail(n);
     a.softmax_pv(stage_buf<ST>(sV0, sV1, sV2));
     if constexpr (!MDIRECT) {
