@@ -19,12 +19,9 @@ import threading
 import torch
 
 from . import _lib, fa
+from .loader import CustomOpsError, FAOps
 
-__all__ = ["ops", "RecsysOps", "CustomOpsError", "mha_fwd_with_mask"]
-
-
-class CustomOpsError(RuntimeError):
-    """Load/dispatch failure (the reference raises the same class name, __init__.py)."""
+__all__ = ["ops", "RecsysOps", "CustomOpsError", "FAOps", "mha_fwd_with_mask"]
 
 
 def _resolve_backend(backend):
@@ -47,38 +44,85 @@ def _resolve_backend(backend):
 
 
 class RecsysOps:
-    """Lazy facade over the op groups. Only the ``fa`` group exists here."""
+    """Lazy facade over the op groups (reference ``RecsysOps``, recsys.py:451-640).
+    Only the ``fa`` group exists here.
 
-    _GROUPS = ("fa",)
+    Development (``allow_jit=True``, the default): a group loads on first use
+    from the in-tree library (compiled with hipcc if missing). Deployment:
+    ``load_precompiled('fa', path)`` validates and loads an exported library and
+    switches the facade to strict mode, in which nothing is ever compiled and
+    an unloaded group raises."""
+
+    _GROUP_CLASSES = {"fa": FAOps}
     _OP_TO_GROUP = {"mha_fwd_with_mask": "fa"}
 
-    def __init__(self) -> None:
+    def __init__(self, *, allow_jit: bool = True) -> None:
         self._lock = threading.RLock()
-        self._state = {}     # group -> "loaded" | "failed"
-        self._errors = {}
+        self._groups: dict = {}     # group -> FAOps instance
+        self._allow_jit = True
+        self.configure(allow_jit=allow_jit)
+
+    @property
+    def allow_jit(self) -> bool:
+        return self._allow_jit
+
+    @allow_jit.setter
+    def allow_jit(self, value: bool) -> None:
+        self.configure(allow_jit=value)
+
+    def configure(self, *, allow_jit: bool) -> "RecsysOps":
+        """Policy for all current and future groups, without loading any."""
+        if not isinstance(allow_jit, bool):
+            raise TypeError("allow_jit must be a bool")
+        with self._lock:
+            self._allow_jit = allow_jit
+            for inst in self._groups.values():
+                inst.configure(allow_jit=allow_jit)
+        return self
+
+    def disable_jit(self) -> "RecsysOps":
+        return self.configure(allow_jit=False)
 
     def _validate_group(self, name: str) -> None:
-        if name not in self._GROUPS:
-            raise ValueError(f"unknown group {name!r}; available: {sorted(self._GROUPS)}")
+        if name not in self._GROUP_CLASSES:
+            raise ValueError(f"unknown group {name!r}; available: {sorted(self._GROUP_CLASSES)}")
 
-    def _group(self, name: str) -> None:
+    def _group(self, name: str) -> FAOps:
         with self._lock:
             self._validate_group(name)
-            if self._state.get(name) == "loaded":
-                return
-            try:
-                _lib.load()
-                fa.register()
-            except Exception as e:  # keep the reason, fail loudly at use
-                self._state[name] = "failed"
-                self._errors[name] = str(e)
-                raise CustomOpsError(f"group {name!r} failed to load: {e}") from e
-            self._state[name] = "loaded"
-            self._errors.pop(name, None)
+            if not self._allow_jit:
+                inst = self._groups.get(name)
+                if inst is None or not inst.is_available():
+                    err = inst.load_error() if inst is not None else None
+                    raise CustomOpsError(
+                        f"JIT is disabled for group {name!r}; call "
+                        f"load_precompiled({name!r}, library_path, metadata_path=None) first."
+                        + (f" Previous error: {err}" if err else ""))
+                return inst
+            if name not in self._groups:
+                self._groups[name] = self._GROUP_CLASSES[name](allow_jit=True)
+            inst = self._groups[name]
+            if not inst.is_available():
+                inst.load()
+            return inst
+
+    def load_precompiled(self, group: str, library_path, metadata_path=None) -> "RecsysOps":
+        """Validate and load an exported library; disables compiling for all groups."""
+        with self._lock:
+            self._validate_group(group)
+            self.configure(allow_jit=False)
+            if group not in self._groups:
+                self._groups[group] = self._GROUP_CLASSES[group](allow_jit=False)
+            self._groups[group].load_precompiled(library_path, metadata_path)
+        return self
 
     def ensure_loaded(self, *names) -> "RecsysOps":
-        for name in (names or self._GROUPS):
-            self._group(name)
+        targets = names or tuple(self._GROUP_CLASSES)
+        with self._lock:
+            for name in targets:
+                self._validate_group(name)
+            for name in targets:
+                self._group(name)
         return self
 
     def load(self) -> "RecsysOps":
@@ -87,28 +131,36 @@ class RecsysOps:
     @property
     def groups(self) -> dict:
         with self._lock:
-            return {g: self._state.get(g, "not_loaded") for g in self._GROUPS}
+            return {g: ("loaded" if self._groups[g].is_available() else "failed")
+                    if g in self._groups else "not_loaded" for g in self._GROUP_CLASSES}
 
     def is_available(self, group: str | None = None) -> bool:
-        """True when the device is usable and the requested (or every) group loads."""
-        if group is not None:
-            self._validate_group(group)
-        if not torch.cuda.is_available():
-            return False
-        try:
-            self.ensure_loaded(*( [group] if group else []))
-        except CustomOpsError:
-            return False
-        return True
+        """True when the device is usable and the requested (or every) group loads.
+        In strict mode a read-only query."""
+        with self._lock:
+            if group is not None:
+                self._validate_group(group)
+            if not torch.cuda.is_available():
+                return False
+            if not self._allow_jit:
+                names = [group] if group else list(self._groups)
+                return bool(names) and all(
+                    n in self._groups and self._groups[n].is_available() for n in names)
+            try:
+                self.ensure_loaded(*([group] if group else []))
+            except CustomOpsError:
+                return False
+            return True
 
     def load_error(self, group: str | None = None):
         with self._lock:
             if group is not None:
                 self._validate_group(group)
-                return self._errors.get(group)
-            for g in self._GROUPS:
-                if g in self._errors:
-                    return self._errors[g]
+                inst = self._groups.get(group)
+                return inst.load_error() if inst is not None else None
+            for inst in self._groups.values():
+                if not inst.is_available():
+                    return inst.load_error()
         return None
 
     def mha_fwd_with_mask(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -126,10 +178,11 @@ class RecsysOps:
             raise AttributeError(name)
         raise AttributeError(
             f"No op '{name}' in recsys_ops. Available ops: {sorted(self._OP_TO_GROUP)} "
-            f"(groups: {sorted(self._GROUPS)})")
+            f"(groups: {sorted(self._GROUP_CLASSES)})")
 
     def __repr__(self) -> str:
-        return f"RecsysOps(namespace='recsys_ops', backend='hip', groups={self.groups})"
+        return (f"RecsysOps(lazy, allow_jit={self.allow_jit}, namespace='recsys_ops', "
+                f"backend='hip', groups={self.groups})")
 
 
 ops = RecsysOps()

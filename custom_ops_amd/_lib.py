@@ -68,25 +68,38 @@ class Params(ctypes.Structure):
 
 _lock = threading.Lock()
 _lib = None
+_lib_file: str | None = None
 _load_error: str | None = None
 
 
-def load() -> ctypes.CDLL:
-    """Load the library once; raise RuntimeError (with the reason) if it is absent."""
-    global _lib, _load_error
+def load(path: str | None = None) -> ctypes.CDLL:
+    """Open the library once per process; raise RuntimeError (with the reason)
+    if it is absent or incompatible.
+
+    ``path`` names the file to open (default: the in-tree build, or
+    MI355_FA_LIB). Once a library is open, asking for a different file raises:
+    one library serves the process."""
+    global _lib, _load_error, _lib_file
     with _lock:
+        want = os.path.realpath(path if path is not None else lib_path())
         if _lib is not None:
+            if path is not None and want != _lib_file:
+                raise RuntimeError(f"{_lib_file} is already loaded in this process; "
+                                   f"cannot also load {want}")
             return _lib
-        LIB_PATH = lib_path()
-        if not os.path.exists(LIB_PATH):
-            _load_error = (f"{LIB_PATH} is missing: build it with `python -m custom_ops_amd.build` "
+        if not os.path.exists(want):
+            _load_error = (f"{want} is missing: build it with `python -m custom_ops_amd.build` "
                            f"(or __graft_entry__.build())")
             raise RuntimeError(_load_error)
         try:
-            lib = ctypes.CDLL(LIB_PATH)
+            lib = ctypes.CDLL(want)
         except OSError as e:
-            _load_error = f"failed to load {LIB_PATH}: {e}"
+            _load_error = f"failed to load {want}: {e}"
             raise RuntimeError(_load_error) from e
+        missing = [n for n in EXPORTED if not hasattr(lib, n)]
+        if missing:
+            _load_error = f"{want} does not export {missing}"
+            raise RuntimeError(_load_error)
         P = ctypes.POINTER(Params)
         lib.mi355_fa_fwd.argtypes = [P, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
         lib.mi355_fa_fwd.restype = ctypes.c_int
@@ -102,11 +115,17 @@ def load() -> ctypes.CDLL:
         lib.mi355_fa_build_info.restype = ctypes.c_char_p
         ver = lib.mi355_fa_abi_version()
         if ver != ABI_VERSION:
-            _load_error = f"{LIB_PATH}: ABI version {ver}, expected {ABI_VERSION}; rebuild it"
+            _load_error = f"{want}: ABI version {ver}, expected {ABI_VERSION}; rebuild it"
             raise RuntimeError(_load_error)
         _lib = lib
+        _lib_file = want
         _load_error = None
         return lib
+
+
+def loaded_path() -> str | None:
+    """The file this process opened, if any."""
+    return _lib_file if _lib is not None else None
 
 
 def load_error() -> str | None:

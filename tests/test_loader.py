@@ -1,0 +1,223 @@
+"""CPU tests of deployment loading (custom_ops_amd/loader.py): offline build with
+a metadata sidecar, validated precompiled load, strict (no-compile) policy and
+fail-closed dispatcher ownership. They follow the intent of the reference's
+tests/test_custom_ops_loading.py (fresh processes for every dispatcher state,
+rejection before the library is opened, copies and untracked registrations
+refused), for this build's ctypes-loaded C-ABI library.
+"""
+import json
+import os
+import shutil
+import subprocess
+import sys
+import textwrap
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def run_py(code: str, timeout: int = 300):
+    """Run `code` in a fresh interpreter (fresh dispatcher) from the repo root."""
+    env = dict(os.environ, PYTHONPATH=ROOT)
+    env.pop("MI355_FA_LIB", None)
+    res = subprocess.run([sys.executable, "-c", textwrap.dedent(code)], cwd=ROOT, env=env,
+                         capture_output=True, text=True, timeout=timeout)
+    return res.returncode, res.stdout, res.stderr
+
+
+@pytest.fixture(scope="module")
+def exported(tmp_path_factory):
+    """One offline build shared by the tests (hipcc cross-compiles, no GPU)."""
+    from custom_ops_amd.loader import FAOps
+    out = tmp_path_factory.mktemp("export")
+    lib = FAOps().build(out)
+    return lib
+
+
+def copy_pair(lib, dst_dir):
+    dst_dir.mkdir(parents=True, exist_ok=True)
+    dst = dst_dir / lib.name
+    shutil.copy2(lib, dst)
+    shutil.copy2(str(lib) + ".json", str(dst) + ".json")
+    return dst
+
+
+def test_build_exports_library_and_sidecar_without_loading(exported):
+    from custom_ops_amd import _lib
+    from custom_ops_amd.loader import _file_sha256
+    md = json.loads(open(str(exported) + ".json").read())
+    assert md["producer"] == "custom_ops_amd" and md["namespace"] == "recsys_ops"
+    assert md["offload_arch"] == ["gfx950"]
+    assert md["schemas"] == {"recsys_ops::mha_fwd_with_mask":
+                             "recsys_ops::mha_fwd_with_mask(Tensor q, Tensor k, Tensor v, "
+                             "Tensor mask) -> Tensor"}
+    assert md["library"]["sha256"] == _file_sha256(exported)
+    assert md["library"]["size"] == exported.stat().st_size
+    assert md["compatibility"]["abi_version"] == _lib.ABI_VERSION
+    assert "-packed-fp32-ops" in md["build"]["flags"]
+    assert len(md["source_fingerprint"]) == 64 and len(md["build_fingerprint"]) == 64
+
+
+def test_precompiled_load_in_fresh_process_is_strict(exported):
+    rc, out, err = run_py(f"""
+        import torch
+        from custom_ops_amd import ops, CustomOpsError
+        ops.load_precompiled("fa", {str(exported)!r})
+        assert not ops.allow_jit
+        assert ops.groups == {{"fa": "loaded"}}, ops.groups
+        s = str(torch.ops.recsys_ops.mha_fwd_with_mask.default._schema)
+        assert s.startswith("recsys_ops::mha_fwd_with_mask(Tensor q"), s
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(
+            "recsys_ops::mha_fwd_with_mask", "Meta")
+        from custom_ops_amd import _lib
+        import os
+        assert _lib.loaded_path() == os.path.realpath({str(exported)!r})
+        # the same file again is idempotent
+        ops.load_precompiled("fa", {str(exported)!r})
+        print("OK")
+    """)
+    assert rc == 0 and "OK" in out, err[-3000:]
+
+
+def test_strict_facade_never_compiles_or_opens_the_dev_library():
+    rc, out, err = run_py("""
+        from custom_ops_amd import ops, CustomOpsError
+        from custom_ops_amd import build, _lib
+        called = []
+        build.build = lambda *a, **k: called.append(1)
+        ops.disable_jit()
+        try:
+            ops.ensure_loaded("fa")
+        except CustomOpsError as e:
+            assert "load_precompiled" in str(e), e
+        else:
+            raise SystemExit("strict ensure_loaded did not raise")
+        assert ops.is_available("fa") is False
+        assert not called and _lib.loaded_path() is None
+        print("OK")
+    """)
+    assert rc == 0 and "OK" in out, err[-3000:]
+
+
+@pytest.mark.parametrize("field,value,msg", [
+    ("namespace", "other_ops", "namespace mismatch"),
+    ("format_version", 99, "format_version mismatch"),
+    ("build_version", 1, "build_version mismatch"),
+    ("required_ops", ["mha_fwd"], "required_ops mismatch"),
+    ("offload_arch", ["gfx942", "gfx950"], "build fingerprint"),
+])
+def test_metadata_mismatch_rejected_before_open(exported, tmp_path, field, value, msg):
+    lib = copy_pair(exported, tmp_path / "m")
+    side = str(lib) + ".json"
+    md = json.loads(open(side).read())
+    md[field] = value
+    open(side, "w").write(json.dumps(md))
+    rc, out, err = run_py(f"""
+        from custom_ops_amd.loader import FAOps, CustomOpsError
+        from custom_ops_amd import _lib
+        try:
+            FAOps().load_precompiled({str(lib)!r})
+        except CustomOpsError as e:
+            print("ERR", e)
+        assert _lib.loaded_path() is None      # rejected before dlopen
+    """)
+    assert rc == 0 and "ERR" in out and msg in out, (out, err[-2000:])
+
+
+def test_schema_contract_and_compat_mismatch(exported, tmp_path):
+    from custom_ops_amd.loader import _metadata_fingerprint
+    for field, mutate, msg in [
+        ("schemas", lambda md: md["schemas"].update(
+            {"recsys_ops::mha_fwd_with_mask": "recsys_ops::mha_fwd_with_mask(Tensor q) -> Tensor"}),
+         "schema contract"),
+        ("compatibility", lambda md: md["compatibility"].update({"abi_version": 2}),
+         "compatibility mismatch (abi_version)"),
+        ("compatibility", lambda md: md["compatibility"].update({"torch": "1.13"}),
+         "compatibility mismatch (torch)"),
+        ("offload_arch", lambda md: md.update({"offload_arch": ["GFX950"]}), "invalid offload"),
+    ]:
+        lib = copy_pair(exported, tmp_path / field / msg[:8].replace(" ", "_"))
+        side = str(lib) + ".json"
+        md = json.loads(open(side).read())
+        mutate(md)
+        md["build_fingerprint"] = _metadata_fingerprint(md)   # a consistent but wrong sidecar
+        open(side, "w").write(json.dumps(md))
+        from custom_ops_amd.loader import FAOps, CustomOpsError
+        with pytest.raises(CustomOpsError, match=msg.replace("(", r"\(").replace(")", r"\)")):
+            FAOps().load_precompiled(lib)
+
+
+def test_visible_target_mismatch_rejected(exported, monkeypatch):
+    from custom_ops_amd import loader
+    monkeypatch.setattr(loader, "_visible_archs", lambda: {"gfx942"})
+    with pytest.raises(loader.CustomOpsError, match="target mismatch"):
+        loader.FAOps().load_precompiled(exported)
+
+
+def test_modified_or_missing_files_rejected(exported, tmp_path):
+    from custom_ops_amd.loader import FAOps, CustomOpsError
+    lib = copy_pair(exported, tmp_path / "t")
+    with open(lib, "r+b") as f:          # same size, one byte changed
+        f.seek(4096)
+        b = f.read(1)
+        f.seek(4096)
+        f.write(bytes([b[0] ^ 0xFF]))
+    with pytest.raises(CustomOpsError, match="hash/size mismatch"):
+        FAOps().load_precompiled(lib)
+    lib2 = copy_pair(exported, tmp_path / "n")
+    os.remove(str(lib2) + ".json")
+    with pytest.raises(CustomOpsError, match="failed"):
+        FAOps().load_precompiled(lib2)
+    with pytest.raises(CustomOpsError):
+        FAOps().load_precompiled(tmp_path / "absent.so")
+
+
+def test_copy_of_loaded_library_is_a_dispatcher_conflict(exported, tmp_path):
+    other = copy_pair(exported, tmp_path / "copy")
+    rc, out, err = run_py(f"""
+        from custom_ops_amd.loader import FAOps, CustomOpsError
+        FAOps().load_precompiled({str(exported)!r})
+        try:
+            FAOps().load_precompiled({str(other)!r})
+        except CustomOpsError as e:
+            print("ERR", e)
+    """)
+    assert rc == 0 and "dispatcher library conflict" in out, (out, err[-2000:])
+
+
+def test_untracked_registration_is_fail_closed(exported):
+    rc, out, err = run_py(f"""
+        import torch
+        lib = torch.library.Library("recsys_ops", "FRAGMENT")
+        lib.define("mha_fwd_with_mask(Tensor q, Tensor k, Tensor v, Tensor mask) -> Tensor")
+        from custom_ops_amd.loader import FAOps, CustomOpsError
+        from custom_ops_amd import _lib
+        try:
+            FAOps().load_precompiled({str(exported)!r})
+        except CustomOpsError as e:
+            print("ERR", e)
+        assert _lib.loaded_path() is None
+    """)
+    assert rc == 0 and "untracked library" in out, (out, err[-2000:])
+
+
+def test_build_refuses_to_overwrite_a_loaded_library(exported):
+    rc, out, err = run_py(f"""
+        from custom_ops_amd.loader import FAOps, CustomOpsError
+        FAOps().load_precompiled({str(exported)!r})
+        try:
+            FAOps().build({str(exported.parent)!r})
+        except CustomOpsError as e:
+            print("ERR", e)
+    """, timeout=600)
+    assert rc == 0 and "cannot overwrite a library loaded" in out, (out, err[-2000:])
+
+
+def test_policy_is_explicit_bool():
+    from custom_ops_amd import RecsysOps
+    from custom_ops_amd.loader import FAOps
+    for obj in (RecsysOps(), FAOps()):
+        with pytest.raises(TypeError):
+            obj.configure(allow_jit="no")
+        assert obj.disable_jit().allow_jit is False
