@@ -130,6 +130,33 @@ def cpu_baseline(cfg, seconds):
     }
 
 
+def cpu_configs(seconds_each):
+    """The same CPU path on every BASELINE config: whole (b, h) heads for up to
+    ``seconds_each`` each, extrapolated to the full workload (cfg1, the
+    reference's CPU plumbing case, runs whole)."""
+    import torch
+    from custom_ops_amd.workloads import CONFIGS, make_inputs
+    from oracle.oracle import torch_math_cpu
+    out = {}
+    for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5"):
+        c = CONFIGS[name]
+        q, k, v, m = make_inputs(c)
+        heads = [(b, h) for b in range(c.B) for h in range(c.H)]
+        torch_math_cpu(q, k, v, m, heads=heads[:1])
+        done = 0
+        t0 = time.perf_counter()
+        while done < len(heads) and (done == 0 or time.perf_counter() - t0 < seconds_each):
+            torch_math_cpu(q, k, v, m, heads=[heads[done]])
+            done += 1
+        el = time.perf_counter() - t0
+        us_full = el / done * len(heads) * 1e6
+        out[name] = {"us": round(us_full, 1),
+                     "tflops": round(c.flops / (us_full * 1e-6) / 1e12, 5),
+                     "heads_timed": f"{done}/{len(heads)}",
+                     "extrapolated": done < len(heads)}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -239,6 +266,7 @@ def main():
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+        result["cpu_baseline"]["configs"] = cpu_configs(2.0)
 
     print(json.dumps(result), flush=True)
 
