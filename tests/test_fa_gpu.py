@@ -239,6 +239,42 @@ def test_dead_mask_blocks(ops, gpu, monkeypatch, kind, waves, splits):
     assert torch.all(out.permute(0, 2, 1, 3)[dead_rows] == 0)
 
 
+def _sweep_cases(n=48, seed=2024):
+    """Seeded random shapes over the op's whole contract."""
+    import random
+    rnd = random.Random(seed)
+    kinds = ["zero", "causal", "random", "block", "all_masked_row", "inf_random", "bias",
+             "full_row"]
+    cases = []
+    for i in range(n):
+        d = rnd.choice([64, 128])
+        hk = rnd.choice([1, 2, 4])
+        h = hk * rnd.choice([1, 2, 4])
+        b = rnd.choice([1, 2, 3])
+        sq = rnd.choice([1, 2, 17, 64, 100, 129, 255, 256, 257, 400, 513])
+        sk = rnd.choice([1, 5, 8, 31, 64, 65, 127, 200, 511, 777, 1024, 1500, 3001])
+        dtype = rnd.choice(["bf16", "fp16"])
+        kind = rnd.choice(kinds)
+        pad_r, pad_c = rnd.choice([(0, 0), (0, 0), (3, 0), (0, 5), (7, 8)])
+        splits = rnd.choice([0, 0, 0, 1, 2, 5])
+        cases.append((i, b, h, hk, sq, sk, d, dtype, kind, pad_r, pad_c, splits))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: f"sweep{c[0]}")
+def test_random_shape_sweep(ops, gpu, case):
+    """Randomised (seeded) coverage of the contract: MHA and GQA, d 64/128,
+    bf16/fp16, ragged Sq/Sk, pre-padded masks with trap values, every mask
+    kind, automatic and forced split counts."""
+    i, b, h, hk, sq, sk, d, dtype, kind, pad_r, pad_c, splits = case
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    c = make_case(b, h, hk, sq, sk, d, kind, dt, seed=1000 + i, extra_rows=pad_r,
+                  extra_cols=pad_c)
+    out, _ = run(ops, c, gpu, f"sweep{i} {case[1:]}", num_splits=splits)
+    rows_dead = torch.isinf(c[3][:, 0, :sq, :sk].float()).all(-1)       # [b, sq]
+    assert torch.all(out.permute(0, 2, 1, 3)[rows_dead.to(gpu)] == 0)
+
+
 def test_all_masked_everything_split(ops, gpu):
     q, k, v, m = make_case(1, 2, 2, 64, 4096, 128, "zero", torch.bfloat16)
     m = torch.full_like(m, float("-inf"))
