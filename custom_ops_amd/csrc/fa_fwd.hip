@@ -2,7 +2,7 @@
 //
 // O = softmax(Q·Kᵀ·scale + mask)·V, additive mask broadcast over heads, GQA.
 // Semantics follow the reference op (Defyli/custom_ops):
-//   - mask added to the scaled score, col >= Sk always blocked
+//   - mask·(1/scale) added to the unscaled score q·k, col >= Sk always blocked
 //       csrc/fa/sm89/fa_fwd_kernel.h:284-310
 //   - online softmax with the -inf guards (max == -inf → use 0; l == 0 → output 0)
 //       csrc/fa/common/softmax.h:65-151
@@ -24,6 +24,8 @@
 //   * Oᵀ = Vᵀ·Pᵀ: the Sᵀ accumulators, rounded to bf16/fp16, are directly the
 //     B operand of the PV MFMA (no LDS round trip for P). The A operand Vᵀ is
 //     read from row-major V in LDS with ds_read_b64_tr_b16.
+//   * The widened, pre-scaled mask tile initialises the QK accumulators, so no
+//     pass over the scores sits between the two GEMMs except the row max.
 //   * K, V and the mask tile of tile n+1 go HBM → LDS by buffer_load ... lds
 //     (no VGPR staging) while tile n computes; double-buffered LDS, one barrier
 //     per tile. XOR swizzles keep every LDS read conflict-free.
@@ -32,9 +34,9 @@
 //   * Sk tails are predicated in-kernel (buffer-resource bounds return 0 for
 //     K/V rows past Sk, scores of those keys are forced to -inf); unaligned mask
 //     rows (mask row stride % 8 != 0) are loaded through registers.
-//   * Linear workgroup ids are remapped so that consecutive logical tiles
-//     (the m-blocks of one head, the heads of one GQA group) land on the same
-//     XCD and share its L2.
+//   * Linear workgroup ids are remapped so that consecutive logical tiles land
+//     on the same XCD and share its L2: the m-blocks of one head (K/V reuse),
+//     or for grids with few m-blocks the heads of one batch (mask reuse).
 
 #include <hip/hip_runtime.h>
 
@@ -60,8 +62,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBN = 64;
-constexpr int kMaxLive = 2048;   // KV tiles one workgroup can list (Sk per split <= 131072)       // keys per KV tile
+constexpr int kBN = 64;          // keys per KV tile
 constexpr int kMaxSplits = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -599,39 +600,24 @@ struct Attn {
   }
 };
 
-template <int I>
-__device__ __forceinline__ uint16_t* stage_buf(uint16_t* b0, uint16_t* b1, uint16_t* b2) {
-  if constexpr (I == 0) return b0;
-  else if constexpr (I == 1) return b1;
-  else return b2;
-}
-
-// Software pipeline over KV tiles with NS LDS stages (2 or 3).
-// Iteration over tile n, stage ST = (n - nb) % NS holding K(n), V(n), mask(n):
-//   wait until tile n's loads have landed (tiles n+1 .. n+NS-2 may still be in
-//   flight) + barrier; issue K, V, mask of tile n+NS-1 into the stage freed by
-//   tile n-1; Sᵀ(n) = K(n)·Qᵀ; + mask(n); softmax(n) fused with
-//   Oᵀ += Vᵀ(n)·Pᵀ(n). One barrier per tile. (Skipping tiles whose mask block
-//   is all -inf measured slower on masks without such blocks: the tile's DMA,
-//   wait and barrier remain, and the test costs LDS reads and VALU.)
+// Software pipeline over KV tiles, two LDS stages per stream. Iteration over
+// tile n (stage ST = (n - nb) % 2 holds K(n), V(n), mask(n)):
+//   wait until tile n has landed + barrier; issue K and mask of tile n+1 into
+//   stage ST^1 (tile n-1's, read in the previous iteration);
+//   u = mask(n)·(1/scale) + K(n)·Qᵀ; issue V of tile n+1; softmax(n) fused
+//   with Oᵀ += Vᵀ(n)·Pᵀ(n). One barrier per tile.
 // Unaligned mask rows go through registers one tile ahead instead (loaded
-// before the DMAs so waiting for them does not wait for the DMAs).
+// before the DMAs so waiting for them does not wait for the DMAs) and are
+// stored to the next stage at the end of the iteration.
+// Measured and not kept: a third stage (also with a single mask buffer to fit
+// 8 waves), skipping all -inf mask blocks, persistent workgroups.
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
   typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
-  // 3 stages measured no faster than 2 for the 4-wave kernel (cfg4/cfg5 shapes)
-  // and cost 48 KiB of LDS, so both variants run 2 stages.
-  constexpr int NS = 2;
-  // LDS-DMA instructions per wave per tile
-  constexpr int kL = 2 * G::kKWaveLoads + (MDIRECT ? G::kMWaveLoads : 0);
-  static_assert(kL * (NS - 2) < 64, "vmcnt range");
   __shared__ __align__(16) uint16_t sK0[G::kKElems], sK1[G::kKElems];
   __shared__ __align__(16) uint16_t sV0[G::kVElems], sV1[G::kVElems];
   __shared__ __align__(16) uint16_t sM0[G::kMElems], sM1[G::kMElems];
-  __shared__ __align__(16) uint16_t sK2[NS == 3 ? G::kKElems : 8];
-  __shared__ __align__(16) uint16_t sV2[NS == 3 ? G::kVElems : 8];
-  __shared__ __align__(16) uint16_t sM2[NS == 3 ? G::kMElems : 8];
 
   const TileIdx ti = tile_index<G::kBM>(p);
   A a(p);
@@ -645,74 +631,50 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads) {
     reinterpret_cast<u32x4*>(sV0)[i] = u32x4{0u, 0u, 0u, 0u};
     reinterpret_cast<u32x4*>(sV1)[i] = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (NS == 3) reinterpret_cast<u32x4*>(sV2)[i] = u32x4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
   const int cnt = ne - nb;
-  auto tile = [&](int i) -> int { return nb + i; };   // visit order
-  // prologue: tiles 0 .. NS-2 of the visit order
   if (cnt > 0) {
-    const int t0 = tile(0);
-    a.issue_m(t0, sM0);
-    a.issue_k(t0, sK0);
-    a.issue_v(t0, sV0);
-  }
-  if constexpr (NS == 3) {
-    if (1 < cnt) {
-      const int t1 = tile(1);
-      if constexpr (MDIRECT) a.issue_m(t1, sM1);
-      a.issue_k(t1, sK1);
-      a.issue_v(t1, sV1);
-    }
+    a.issue_m(nb, sM0);
+    a.issue_k(nb, sK0);
+    a.issue_v(nb, sV0);
   }
   a.load_q(qrow, rq);
   if (cnt > 0) a.commit_m(sM0);
 
-  auto iter = [&](auto stc, int i) {
+  auto iter = [&](auto stc, int n) {
     constexpr int ST = decltype(stc)::value;
-    constexpr int NX = (ST + NS - 1) % NS;   // receives visit i+NS-1
-    constexpr int N1 = (ST + 1) % NS;        // holds visit i+1
-    const int n = tile(i);
-    if constexpr (NS == 3) {
-      if (i + 1 < cnt) wait_vmcnt<kL>();
-      else wait_vmcnt<0>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    uint16_t* kH = ST ? sK1 : sK0;
+    uint16_t* kN = ST ? sK0 : sK1;
+    uint16_t* mH = ST ? sM1 : sM0;
+    uint16_t* mN = ST ? sM0 : sM1;
+    uint16_t* vH = ST ? sV1 : sV0;
+    uint16_t* vN = ST ? sV0 : sV1;
+    const bool more = n + 1 < ne;
+    wait_vmcnt<0>();
     __syncthreads();
     if constexpr (!MDIRECT) {
-      if (i + 1 < cnt) a.issue_m(tile(i + 1), nullptr);   // into registers
+      if (more) a.issue_m(n + 1, nullptr);   // into registers
     }
-    if (i + NS - 1 < cnt) {
-      const int nx = tile(i + NS - 1);
-      if constexpr (MDIRECT) a.issue_m(nx, stage_buf<NX>(sM0, sM1, sM2));
-      a.issue_k(nx, stage_buf<NX>(sK0, sK1, sK2));
+    if (more) {
+      if constexpr (MDIRECT) a.issue_m(n + 1, mN);
+      a.issue_k(n + 1, kN);
     }
-    a.mask_init(stage_buf<ST>(sM0, sM1, sM2));
-    a.qk(stage_buf<ST>(sK0, sK1, sK2));
-    if (i + NS - 1 < cnt) a.issue_v(tile(i + NS - 1), stage_buf<NX>(sV0, sV1, sV2));
+    a.mask_init(mH);
+    a.qk(kH);
+    if (more) a.issue_v(n + 1, vN);
     a.apply_tail(n);
-    a.softmax_pv(stage_buf<ST>(sV0, sV1, sV2));
+    a.softmax_pv(vH);
     if constexpr (!MDIRECT) {
-      if (i + 1 < cnt) a.commit_m(stage_buf<N1>(sM0, sM1, sM2));
+      if (more) a.commit_m(mN);
     }
   };
-  int i = 0;
-  if constexpr (NS == 3) {
-    for (; i + 2 < cnt; i += 3) {
-      iter(std::integral_constant<int, 0>{}, i);
-      iter(std::integral_constant<int, 1>{}, i + 1);
-      iter(std::integral_constant<int, 2>{}, i + 2);
-    }
-    if (i < cnt) iter(std::integral_constant<int, 0>{}, i);
-    if (i + 1 < cnt) iter(std::integral_constant<int, 1>{}, i + 1);
-  } else {
-    for (; i + 1 < cnt; i += 2) {
-      iter(std::integral_constant<int, 0>{}, i);
-      iter(std::integral_constant<int, 1>{}, i + 1);
-    }
-    if (i < cnt) iter(std::integral_constant<int, 0>{}, i);
+  int n = nb;
+  for (; n + 1 < ne; n += 2) {
+    iter(std::integral_constant<int, 0>{}, n);
+    iter(std::integral_constant<int, 1>{}, n + 1);
   }
+  if (n < ne) iter(std::integral_constant<int, 0>{}, n);
 
   a.epilogue(ti.b, ti.h, ti.split, qrow);
 }
