@@ -80,6 +80,9 @@ def load(path: str | None = None) -> ctypes.CDLL:
     MI355_FA_LIB). Once a library is open, asking for a different file raises:
     one library serves the process."""
     global _lib, _load_error, _lib_file
+    lib = _lib
+    if lib is not None and path is None:      # per-call fast path: no lock, no path lookup
+        return lib
     with _lock:
         want = os.path.realpath(path if path is not None else lib_path())
         if _lib is not None:
@@ -132,11 +135,22 @@ def load_error() -> str | None:
     return _load_error
 
 
+_tls = threading.local()
+
+
+def _err_buffer() -> ctypes.Array:
+    """Per-thread message buffer, reused across calls (the library writes it only on failure)."""
+    buf = getattr(_tls, "err", None)
+    if buf is None:
+        buf = _tls.err = ctypes.create_string_buffer(512)
+    return buf
+
+
 def fwd(params: Params, stream: int) -> None:
     """Call mi355_fa_fwd; raise RuntimeError carrying the library's message on failure."""
     lib = load()
-    err = ctypes.create_string_buffer(512)
-    rc = lib.mi355_fa_fwd(ctypes.byref(params), ctypes.c_void_p(stream), err, len(err))
+    err = _err_buffer()
+    rc = lib.mi355_fa_fwd(ctypes.byref(params), stream, err, 512)
     if rc != OK:
         raise RuntimeError(err.value.decode(errors="replace") or f"mi355_fa_fwd failed ({rc})")
 

@@ -796,9 +796,10 @@ static int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // fa_mask_sm89_num_splits, csrc/fa/fa_fwd_launch.h:137-170): split only when
 // the grid of row tiles under-fills the chip; K = relative cost of one KV tile
 // in the main kernel, P = per-split cost of the partial write + combine.
-// slots = workgroups resident per CU: the reference's kernel fits 2 per SM
-// (cap_fill = 2·SMs / m-blocks, which the exported mi355_fa_cost_model_splits
-// keeps); the 4-wave kernel here holds 96 KiB of LDS, so 1 per CU.
+// slots = workgroups resident per CU (cap_fill = slots·SMs / m-blocks; the
+// reference's kernel fits 2 per SM). Exported as mi355_fa_cost_model_splits
+// with the reference's constants; the launcher's own plan (make_plan) uses a
+// rule measured on MI355X instead.
 static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int cus,
                              int slots = 2) {
   if (cus <= 0) cus = 1;
@@ -834,9 +835,22 @@ struct Plan {
   size_t o_part_bytes, lse_bytes, ws_bytes;
 };
 
-// Tile plan. BM = 256 rows (8 waves) when that grid fills the chip, alone or
-// with 2..4 KV splits; otherwise BM = 128 (4 waves), with split-KV chosen by
-// the cost model when even that grid leaves CUs idle.
+// Tile plan. Measured on MI355X over small grids (bh 1..64, Sq 1..512,
+// Sk 2k..32k, d 64/128, every workgroup size × split count): the best plan
+// fills the chip with whole rounds of workgroups. 8 waves (BM = 256, two
+// waves per SIMD) beat 4 when the 256-row tiles are mostly real rows and
+// each split keeps >= 16 KV tiles; the split count is then chosen so the
+// grid is one round of CUs. Otherwise 4 waves (BM = 128), with two rounds for
+// d = 64 (its KV tiles are half the bytes, so more workgroups are needed to
+// keep HBM busy) and one for d = 128. Every split keeps >= 4 KV tiles, so the
+// partial write and combine stay small next to the split's own work.
+static int fill_splits(int tiles, int rounds, int num_n, int cus) {
+  int s = (int)lrintf((float)rounds * cus / (float)tiles);
+  const int max_s = num_n / 4 > 1 ? num_n / 4 : 1;
+  if (s > max_s) s = max_s;
+  return s < 1 ? 1 : s;
+}
+
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
   pl.num_n = ceil_div(p->seqlen_k, kBN);
@@ -847,22 +861,19 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
     if (env && atoi(env) > 0) s = atoi(env);
   }
   const int m256 = ceil_div(p->seqlen_q, 256), m128 = ceil_div(p->seqlen_q, 128);
-  const bool big = (float)bh * m256 >= 0.8f * cus;
-  // 8 waves (BM = 256, two waves per SIMD) run far better than 4 (one wave
-  // per SIMD), so a grid of 256-row tiles that is short of the chip is first
-  // topped up with 2..4 KV splits, provided the tiles are mostly real rows and
-  // every split keeps >= 8 KV tiles.
-  int fill8 = 0;
-  if (!big && p->seqlen_q >= 192 * m256) {
-    for (int c = 2; c <= 4 && !fill8; ++c)
-      if ((float)bh * m256 * c >= 0.8f * cus && pl.num_n >= 8 * c) fill8 = c;
+  pl.waves = 4;
+  if (p->seqlen_q >= 192 * m256) {
+    const int s8 = fill_splits(bh * m256, 1, pl.num_n, cus);
+    if (s8 == 1 || pl.num_n >= 16 * s8) {
+      pl.waves = 8;
+      if (s <= 0) s = s8;
+    }
   }
-  if (s <= 0) s = big ? 1 : fill8 ? fill8 : cost_model_splits(bh * m128, pl.num_n, 128, p->d, cus, 1);
+  if (s <= 0) s = fill_splits(bh * m128, p->d == 64 ? 2 : 1, pl.num_n, cus);
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > pl.num_n) s = pl.num_n;
   if (s < 1) s = 1;
   pl.splits = s;
-  pl.waves = ((s == 1 && big) || (fill8 && s == fill8)) ? 8 : 4;
   {   // tuning override of the workgroup size (4 or 8 waves)
     const char* w = getenv("MI355_FA_WAVES");
     if (w && (atoi(w) == 4 || atoi(w) == 8)) pl.waves = atoi(w);

@@ -73,7 +73,7 @@ typedef struct mi355_fa_params {
   int32_t dtype;      /* MI355_FA_FP16 | MI355_FA_BF16 */
   float scale_softmax; /* 1/sqrt(d) in the reference op; any positive value allowed */
 
-  /* Split-KV: 0 = let the cost model choose; >= 1 forces that many splits. */
+  /* Split-KV: 0 = let the library plan it; >= 1 forces that many splits. */
   int32_t num_splits;
   /* Device workspace for split-KV partials (may be NULL when no split is planned). */
   void* workspace;
@@ -84,8 +84,8 @@ typedef struct mi355_fa_params {
  * Returns 0 on success; otherwise writes a NUL-terminated message into err. */
 int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errlen);
 
-/* Number of KV splits the launcher will use for these params (after the cost
- * model, the MI355_FA_NUM_SPLITS override and clamping). */
+/* Number of KV splits the launcher will use for these params (after its plan,
+ * the MI355_FA_NUM_SPLITS override and clamping). */
 int mi355_fa_num_splits(const mi355_fa_params* p);
 
 /* Bytes of workspace mi355_fa_fwd needs for these params (0 when unsplit). */

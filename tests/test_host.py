@@ -116,6 +116,28 @@ def test_cost_model_and_workspace(lib):
     assert _lib.num_splits(p) == 1 and _lib.workspace_bytes(p) == 0
 
 
+
+@pytest.mark.parametrize("b,h,sq,sk,d,splits", [
+    (4, 16, 2048, 2048, 128, 1),      # grid of 256-row tiles already fills 256 CUs
+    (1, 16, 128, 32768, 128, 16),     # 16 tiles of 128 rows -> one round of 256
+    (2, 16, 1000, 4099, 128, 2),      # 128 tiles of 256 rows -> 2 splits
+    (1, 16, 512, 32768, 128, 8),      # 32 tiles of 256 rows -> 8 splits
+    (1, 64, 1, 32768, 64, 8),         # d=64 decode: two rounds of 128-row tiles
+    (1, 4, 512, 32768, 128, 32),
+    (1, 4, 512, 8192, 128, 16),       # 8 waves would leave 4 KV tiles a split: 4 waves, 1 round
+    (1, 1, 1, 256, 128, 1),           # >= 4 KV tiles per split caps the count
+    (1, 1, 1, 1024, 128, 4),
+])
+def test_auto_plan_fills_whole_rounds(lib, b, h, sq, sk, d, splits):
+    """The launcher's own plan on a 256-CU part (no GPU here: the library
+    assumes 256 CUs when none can be queried)."""
+    from custom_ops_amd import _lib
+    p = _params(b=b, h=h, h_k=h, seqlen_q=sq, seqlen_k=sk, d=d, mask_seqlen_q=sq,
+                mask_seqlen_k=sk, q_row_stride=d, k_row_stride=d, v_row_stride=d,
+                o_row_stride=d, mask_row_stride=sk)
+    assert _lib.num_splits(p) == splits
+
+
 def test_torch_op_schema_and_fake():
     import custom_ops_amd
     custom_ops_amd.ops.ensure_loaded()
@@ -155,9 +177,12 @@ def test_validation_messages_on_host():
     from custom_ops_amd import fa
 
     class Fake:
-        def __init__(self, shape, dtype=torch.bfloat16, contig=True):
+        def __init__(self, shape, dtype=torch.bfloat16, contig=True, dev=0, cuda=True):
             self.shape, self.dtype, self._c = torch.Size(shape), dtype, contig
-            self.is_cuda, self.device = True, torch.device("cuda:0")
+            self.is_cuda, self.device = cuda, torch.device("cuda", dev)
+
+        def get_device(self):
+            return self.device.index if self.is_cuda else -1
 
         def is_contiguous(self):
             return self._c
@@ -184,8 +209,16 @@ def test_validation_messages_on_host():
         ((q, k, k, Fake((1, 2, 8, 8))), "mask shape"),
         ((q, k, k, Fake((1, 1, 7, 8))), "mask shape"),
         ((q, k, k, Fake((1, 1, 8, 7))), "mask shape"),
+        ((q, k, k, Fake((1, 1, 8, 8), cuda=False)), "mask must be a CUDA tensor"),
+        ((q, k, k, Fake((1, 1, 8, 8), dev=1)), "same device"),
+        ((q, k, Fake((1, 2, 8, 64), contig=False), m), "v must be contiguous"),
+        ((q, k, k, Fake((1, 1, 8, 8, 1))), "mask must be 4D"),
+        ((q, Fake((1, 0, 8, 64)), Fake((1, 0, 8, 64)), m), "divisible"),
     ]
+    assert fa._valid(q, k, k, m)
     for args, msg in cases:
+        # the one-expression fast path rejects exactly what the ordered checks reject
+        assert not fa._valid(*args), msg
         with pytest.raises(RuntimeError, match=msg):
             fa.validate(*args)
 
