@@ -330,7 +330,7 @@ struct Attn {
     }
 #pragma unroll
     for (int i = 0; i < G::kMWaveLoads; ++i) {
-      const int u = (i * G::kWaves + wave) * 64 + lane;
+      const int u = (wave * G::kMWaveLoads + i) * 64 + lane;   // the wave's own 32 rows
       const int m = u / 8, slot = u % 8;
       m_off[i] = (uint32_t)((ti.m0 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
     }
@@ -389,12 +389,12 @@ struct Attn {
       const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(mbase) + key0 * 2u, mbytes - key0 * 2u);
 #pragma unroll
       for (int i = 0; i < G::kMWaveLoads; ++i)
-        bload16_lds(r, sM + (i * G::kWaves + wave) * 64 * 8, m_off[i]);
+        bload16_lds(r, sM + (wave * G::kMWaveLoads + i) * 64 * 8, m_off[i]);
       return;
     } else {
 #pragma unroll
     for (int i = 0; i < G::kMWaveLoads; ++i) {
-      const int u = (i * G::kWaves + wave) * 64 + lane;
+      const int u = (wave * G::kMWaveLoads + i) * 64 + lane;
       const int c = (u % 8) ^ mask_swz(u / 8);
       const int kc = (int)key0 + c * 8;
       const uint32_t off = m_off[i] + key0 * 2u;
@@ -420,7 +420,7 @@ struct Attn {
     if constexpr (MDIRECT) return;
 #pragma unroll
     for (int i = 0; i < G::kMWaveLoads; ++i) {
-      const int u = (i * G::kWaves + wave) * 64 + lane;
+      const int u = (wave * G::kMWaveLoads + i) * 64 + lane;
       *reinterpret_cast<u32x4*>(sM + u * 8) = mreg[i];
     }
   }
@@ -600,24 +600,26 @@ struct Attn {
   }
 };
 
-// Software pipeline over KV tiles, two LDS stages per stream. Iteration over
-// tile n (stage ST = (n - nb) % 2 holds K(n), V(n), mask(n)):
-//   wait until tile n has landed + barrier; issue K and mask of tile n+1 into
-//   stage ST^1 (tile n-1's, read in the previous iteration);
-//   u = mask(n)·(1/scale) + K(n)·Qᵀ; issue V of tile n+1; softmax(n) fused
-//   with Oᵀ += Vᵀ(n)·Pᵀ(n). One barrier per tile.
-// Unaligned mask rows go through registers one tile ahead instead (loaded
-// before the DMAs so waiting for them does not wait for the DMAs) and are
-// stored to the next stage at the end of the iteration.
-// Measured and not kept: a third stage (also with a single mask buffer to fit
-// 8 waves), skipping all -inf mask blocks, persistent workgroups.
+// Software pipeline over KV tiles, two LDS stages for K and V. Iteration over
+// tile n (stage ST = (n - nb) % 2 holds K(n), V(n); the scores already hold
+// mask(n)·(1/scale)):
+//   wait until tile n has landed + barrier; issue mask and K of tile n+1;
+//   u += K(n)·Qᵀ; issue V of tile n+1; softmax(n) fused with Oᵀ += Vᵀ(n)·Pᵀ(n);
+//   wait for the mask loads only (issued first, so the K/V DMAs may still be in
+//   flight) and widen mask(n+1) into the scores. One barrier per tile.
+// Each wave loads and reads only its own 32 mask rows, so the mask needs one
+// LDS buffer and no barrier, and the next tile's GEMM starts right after the
+// barrier. Aligned rows arrive by LDS DMA; unaligned rows go through registers
+// (element-wise past Sk) and the wave stores them to its rows of the buffer.
+// Measured and not kept: a third K/V stage, skipping all -inf mask blocks,
+// persistent workgroups.
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
   typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
   __shared__ __align__(16) uint16_t sK0[G::kKElems], sK1[G::kKElems];
   __shared__ __align__(16) uint16_t sV0[G::kVElems], sV1[G::kVElems];
-  __shared__ __align__(16) uint16_t sM0[G::kMElems], sM1[G::kMElems];
+  __shared__ __align__(16) uint16_t sM[G::kMElems];
 
   const TileIdx ti = tile_index<G::kBM>(p);
   A a(p);
@@ -635,38 +637,41 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   __syncthreads();
   const int cnt = ne - nb;
   if (cnt > 0) {
-    a.issue_m(nb, sM0);
+    a.issue_m(nb, sM);
     a.issue_k(nb, sK0);
     a.issue_v(nb, sV0);
   }
   a.load_q(qrow, rq);
-  if (cnt > 0) a.commit_m(sM0);
+  if (cnt > 0) {
+    wait_vmcnt<0>();
+    a.commit_m(sM);
+    a.mask_init(sM);
+  }
 
+  // Loads of one iteration, in issue order: the mask's, then K's, then V's.
+  constexpr int kKVLoads = 2 * G::kKWaveLoads;
   auto iter = [&](auto stc, int n) {
     constexpr int ST = decltype(stc)::value;
     uint16_t* kH = ST ? sK1 : sK0;
     uint16_t* kN = ST ? sK0 : sK1;
-    uint16_t* mH = ST ? sM1 : sM0;
-    uint16_t* mN = ST ? sM0 : sM1;
     uint16_t* vH = ST ? sV1 : sV0;
     uint16_t* vN = ST ? sV0 : sV1;
     const bool more = n + 1 < ne;
     wait_vmcnt<0>();
     __syncthreads();
-    if constexpr (!MDIRECT) {
-      if (more) a.issue_m(n + 1, nullptr);   // into registers
-    }
     if (more) {
-      if constexpr (MDIRECT) a.issue_m(n + 1, mN);
+      a.issue_m(n + 1, sM);
       a.issue_k(n + 1, kN);
     }
-    a.mask_init(mH);
     a.qk(kH);
     if (more) a.issue_v(n + 1, vN);
     a.apply_tail(n);
     a.softmax_pv(vH);
-    if constexpr (!MDIRECT) {
-      if (more) a.commit_m(mN);
+    if (more) {
+      wait_vmcnt<kKVLoads>();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);   // keep the mask reads below the wait
+      a.commit_m(sM);
+      a.mask_init(sM);
     }
   };
   int n = nb;
