@@ -107,9 +107,30 @@ __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
 }
 // 16 bytes per lane from the buffer straight into LDS: lane i of the wave lands
-// at lds + 16·i (gfx950 LDS DMA), no VGPR staging.
-__device__ __forceinline__ void bload16_lds(rsrc_t r, uint16_t* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, 0, 0, 0);
+// at lds + 16·i (gfx950 LDS DMA), no VGPR staging. Issued as inline assembly so
+// the compiler does not track the LDS write: it would otherwise wait for every
+// DMA in flight (vmcnt(0)) before each LDS read and each workgroup barrier,
+// which serialises a multi-stage pipeline. Completion is therefore the
+// caller's job: wait_vmcnt for the issuing wave, then wg_barrier for the others.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+// The same buffer descriptor as make_rsrc, as four plain words for the asm.
+__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, kRsrcFlags};
+}
+// LDS byte address of a __shared__ array (folds to a constant after inlining).
+__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
+}
+__device__ __forceinline__ void bload16_lds(i32x4 rs, uint32_t lds_byte, uint32_t voff) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte);
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(m0v), "v"(voff), "s"(rs)
+      : "memory", "m0");
 }
 
 // ── kernel parameters (device copy, passed by value) ──────────────────────────
@@ -169,6 +190,17 @@ __device__ __forceinline__ int key_perm(int r) {   // π within a 32-key block
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);   // no LDS access moves above the wait
+}
+
+// Workgroup barrier for the LDS pipeline: this wave's LDS reads have returned
+// (so no other wave's DMA can overwrite what they read) and nothing moves across.
+// Unlike __syncthreads it does not wait for the LDS DMAs in flight.
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <bool BF16>
@@ -375,10 +407,10 @@ struct Attn {
 
   __device__ __forceinline__ void issue_k(int n, uint16_t* sK) {
     const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.k_rs * 2u;
-    const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(kbase) + sh, kbytes - sh);
+    const i32x4 r = make_rsrc_words(reinterpret_cast<const char*>(kbase) + sh, kbytes - sh);
 #pragma unroll
     for (int i = 0; i < G::kKWaveLoads; ++i)
-      bload16_lds(r, sK + (i * G::kWaves + wave) * 64 * 8, k_off[i]);
+      bload16_lds(r, lds_addr(sK) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), k_off[i]);
   }
 
   // Mask tile n: LDS DMA when rows are 16-byte aligned, else registers
@@ -386,10 +418,10 @@ struct Attn {
   __device__ __forceinline__ void issue_m(int n, uint16_t* sM) {
     const uint32_t key0 = (uint32_t)n * kBN;
     if constexpr (MDIRECT) {
-      const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(mbase) + key0 * 2u, mbytes - key0 * 2u);
+      const i32x4 r = make_rsrc_words(reinterpret_cast<const char*>(mbase) + key0 * 2u, mbytes - key0 * 2u);
 #pragma unroll
       for (int i = 0; i < G::kMWaveLoads; ++i)
-        bload16_lds(r, sM + (wave * G::kMWaveLoads + i) * 64 * 8, m_off[i]);
+        bload16_lds(r, lds_addr(sM) + (uint32_t)((wave * G::kMWaveLoads + i) * 64 * 16), m_off[i]);
       return;
     } else {
 #pragma unroll
@@ -427,10 +459,10 @@ struct Attn {
 
   __device__ __forceinline__ void issue_v(int n, uint16_t* sV) {
     const uint32_t sh = (uint32_t)n * kBN * (uint32_t)p.v_rs * 2u;
-    const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(vbase) + sh, vbytes - sh);
+    const i32x4 r = make_rsrc_words(reinterpret_cast<const char*>(vbase) + sh, vbytes - sh);
 #pragma unroll
     for (int i = 0; i < G::kKWaveLoads; ++i)
-      bload16_lds(r, sV + (i * G::kWaves + wave) * 64 * 8, v_off[i]);
+      bload16_lds(r, lds_addr(sV) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), v_off[i]);
   }
 
   // u = mask·(1/scale) + K·Qᵀ: the widened, pre-scaled mask tile initialises the
@@ -595,30 +627,38 @@ struct Attn {
       }
       if (g == 0)
         p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY
-                                                 : m_run * p.scale + __builtin_amdgcn_logf(l) * 0.69314718f;
+                                                 : __builtin_fmaf(m_run, p.scale, __builtin_amdgcn_logf(l) * 0.69314718f);
     }
   }
 };
 
-// Software pipeline over KV tiles, two LDS stages for K and V. Iteration over
-// tile n (stage ST = (n - nb) % 2 holds K(n), V(n); the scores already hold
+// Software pipeline over KV tiles with NST LDS stages for K and V. Iteration
+// over tile n (stage n % NST holds K(n), V(n); the scores already hold
 // mask(n)·(1/scale)):
-//   wait until tile n has landed + barrier; issue mask and K of tile n+1;
-//   u += K(n)·Qᵀ; issue V of tile n+1; softmax(n) fused with Oᵀ += Vᵀ(n)·Pᵀ(n);
-//   wait for the mask loads only (issued first, so the K/V DMAs may still be in
-//   flight) and widen mask(n+1) into the scores. One barrier per tile.
+//   [NST = 2: wait for tile n's K/V DMAs] barrier (every wave has landed tile
+//   n and left tile n-1's stage); issue mask(n+1) and K(n+NST-1) into tile
+//   n-1's stage; u += K(n)·Qᵀ; issue V(n+NST-1); softmax(n) fused with
+//   Oᵀ += Vᵀ(n)·Pᵀ(n); wait until everything but the newest tile's K/V DMAs
+//   has landed and widen mask(n+1) into the scores. One barrier per tile.
 // Each wave loads and reads only its own 32 mask rows, so the mask needs one
 // LDS buffer and no barrier, and the next tile's GEMM starts right after the
 // barrier. Aligned rows arrive by LDS DMA; unaligned rows go through registers
 // (element-wise past Sk) and the wave stores them to its rows of the buffer.
-// Measured and not kept: a third K/V stage, skipping all -inf mask blocks,
-// persistent workgroups.
+// Measured and not kept: skipping all -inf mask blocks, persistent workgroups.
+#ifndef MI355_FA_STAGES8
+#define MI355_FA_STAGES8 2
+#endif
+#ifndef MI355_FA_STAGES4
+#define MI355_FA_STAGES4 3
+#endif
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
   typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
-  __shared__ __align__(16) uint16_t sK0[G::kKElems], sK1[G::kKElems];
-  __shared__ __align__(16) uint16_t sV0[G::kVElems], sV1[G::kVElems];
+  constexpr int NST = WAVES == 8 ? MI355_FA_STAGES8 : MI355_FA_STAGES4;
+  static_assert(NST == 2 || NST == 3, "two or three stages");
+  __shared__ __align__(16) uint16_t sK[NST][G::kKElems];
+  __shared__ __align__(16) uint16_t sV[NST][G::kVElems];
   __shared__ __align__(16) uint16_t sM[G::kMElems];
 
   const TileIdx ti = tile_index<G::kBM>(p);
@@ -630,20 +670,22 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   const int qrow = ti.m0 + a.wave * 32 + a.l32;
   // Zero the V buffers once: a V row the tail's DMA leaves unwritten then holds
   // 0 or an earlier tile's finite values, and its P is 0, so it adds nothing.
-  for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads) {
-    reinterpret_cast<u32x4*>(sV0)[i] = u32x4{0u, 0u, 0u, 0u};
-    reinterpret_cast<u32x4*>(sV1)[i] = u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads)
+#pragma unroll
+    for (int st = 0; st < NST; ++st) reinterpret_cast<u32x4*>(sV[st])[i] = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
   const int cnt = ne - nb;
-  if (cnt > 0) {
-    a.issue_m(nb, sM);
-    a.issue_k(nb, sK0);
-    a.issue_v(nb, sV0);
+  if (cnt > 0) a.issue_m(nb, sM);
+#pragma unroll
+  for (int j = 0; j < NST - 1; ++j) {
+    if (j < cnt) {
+      a.issue_k(nb + j, sK[j]);
+      a.issue_v(nb + j, sV[j]);
+    }
   }
   a.load_q(qrow, rq);
+  wait_vmcnt<0>();   // Q and the first tiles, on every path into the loop
   if (cnt > 0) {
-    wait_vmcnt<0>();
     a.commit_m(sM);
     a.mask_init(sM);
   }
@@ -651,35 +693,40 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   // Loads of one iteration, in issue order: the mask's, then K's, then V's.
   constexpr int kKVLoads = 2 * G::kKWaveLoads;
   auto iter = [&](auto stc, int n) {
-    constexpr int ST = decltype(stc)::value;
-    uint16_t* kH = ST ? sK1 : sK0;
-    uint16_t* kN = ST ? sK0 : sK1;
-    uint16_t* vH = ST ? sV1 : sV0;
-    uint16_t* vN = ST ? sV0 : sV1;
-    const bool more = n + 1 < ne;
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (more) {
-      a.issue_m(n + 1, sM);
-      a.issue_k(n + 1, kN);
-    }
-    a.qk(kH);
-    if (more) a.issue_v(n + 1, vN);
+    constexpr int ST = decltype(stc)::value;   // (n - nb) % NST
+    constexpr int SF = (ST + NST - 1) % NST;   // stage of tile n + NST - 1 (= n - 1)
+    const bool more = n + 1 < ne, far = n + NST - 1 < ne;
+    if constexpr (NST == 2) wait_vmcnt<0>();
+    wg_barrier();
+    if (more) a.issue_m(n + 1, sM);
+    if (far) a.issue_k(n + NST - 1, sK[SF]);
+    a.qk(sK[ST]);
+    if (far) a.issue_v(n + NST - 1, sV[SF]);
     a.apply_tail(n);
-    a.softmax_pv(vH);
+    a.softmax_pv(sV[ST]);
     if (more) {
-      wait_vmcnt<kKVLoads>();
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);   // keep the mask reads below the wait
+      if (far) wait_vmcnt<kKVLoads>();
+      else wait_vmcnt<0>();
       a.commit_m(sM);
       a.mask_init(sM);
     }
   };
   int n = nb;
-  for (; n + 1 < ne; n += 2) {
-    iter(std::integral_constant<int, 0>{}, n);
-    iter(std::integral_constant<int, 1>{}, n + 1);
+  if constexpr (NST == 2) {
+    for (; n + 1 < ne; n += 2) {
+      iter(std::integral_constant<int, 0>{}, n);
+      iter(std::integral_constant<int, 1>{}, n + 1);
+    }
+    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
+  } else {
+    for (; n + 2 < ne; n += 3) {
+      iter(std::integral_constant<int, 0>{}, n);
+      iter(std::integral_constant<int, 1>{}, n + 1);
+      iter(std::integral_constant<int, 2>{}, n + 2);
+    }
+    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
+    if (n + 1 < ne) iter(std::integral_constant<int, 1>{}, n + 1);
   }
-  if (n < ne) iter(std::integral_constant<int, 0>{}, n);
 
   a.epilogue(ti.b, ti.h, ti.split, qrow);
 }
