@@ -741,25 +741,38 @@ struct CParams {
   int64_t rows;  // B*H*Sq
 };
 
-// Workgroup = kRows rows × D columns; thread = 8 consecutive d-values of a row
-// (one 16-byte load per split). Phase 1 stages the rows' LSEs in LDS and turns
+// Workgroup = one wave = kRows rows × D columns (4 rows for d = 128), so even
+// a small split grid gives hundreds of workgroups; thread = 8 consecutive
+// d-values of a row (one 16-byte load per split). Phase 1 stages the rows' LSEs in LDS and turns
 // them into weights w_s = exp(lse_s − max) / Σ (all-(-inf) row → all weights
-// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 8 splits'
-// loads in flight.
+// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 16 splits'
+// loads in flight, the first 16 issued before phase 1.
+constexpr int kCombineThreads = 64;
 template <int D, bool BF16>
-__global__ __launch_bounds__(256) void fa_combine_kernel(const CParams p) {
+__global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CParams p) {
   typedef typename Elt<BF16>::v8 V8;
-  constexpr int kTPR = D / 8;              // threads per row
-  constexpr int kRows = 256 / kTPR;        // rows per workgroup
+  constexpr int kTPR = D / 8;                     // threads per row
+  constexpr int kRows = kCombineThreads / kTPR;   // rows per workgroup
+  constexpr int kBatch = 16;                      // splits' loads in flight per thread
   __shared__ float sw[kMaxSplits * kRows];
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
   const int64_t slab = p.rows;
   const int S = p.num_splits;
-  for (int i = tid; i < S * kRows; i += 256) {
-    const int s = i / kRows, r = i % kRows;
-    const int64_t row = row0 + r;
-    sw[i] = (row < p.rows) ? p.lse_part[s * slab + row] : -INFINITY;
+  const int r = tid / kTPR;
+  const int c8 = tid % kTPR;
+  const int64_t row = row0 + r;
+  const bool live = row < p.rows;
+  const uint16_t* src = p.o_part + row * D + c8 * 8;
+  // The first batch of partial rows is requested before the LSE round trip.
+  u32x4 raw[kBatch];
+#pragma unroll
+  for (int u = 0; u < kBatch; ++u)
+    if (live && u < S) raw[u] = *reinterpret_cast<const u32x4*>(src + (int64_t)u * slab * D);
+  for (int i = tid; i < S * kRows; i += kCombineThreads) {
+    const int s = i / kRows, rr = i % kRows;
+    const int64_t lrow = row0 + rr;
+    sw[i] = (lrow < p.rows) ? p.lse_part[s * slab + lrow] : -INFINITY;
   }
   __syncthreads();
   if (tid < kRows) {
@@ -776,19 +789,17 @@ __global__ __launch_bounds__(256) void fa_combine_kernel(const CParams p) {
     for (int s = 0; s < S; ++s) sw[s * kRows + tid] *= inv;
   }
   __syncthreads();
-  const int r = tid / kTPR;
-  const int c8 = tid % kTPR;
-  const int64_t row = row0 + r;
-  if (row >= p.rows) return;
-  const uint16_t* src = p.o_part + row * D + c8 * 8;
+  if (!live) return;
   f32x8 acc = {};
-  for (int s0 = 0; s0 < S; s0 += 8) {
-    u32x4 raw[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+  for (int u = 0; u < kBatch; ++u)
+    if (u < S) acc += sw[u * kRows + r] * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
+  for (int s0 = kBatch; s0 < S; s0 += kBatch) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
       if (s0 + u < S) raw[u] = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + u) * slab * D);
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kBatch; ++u)
       if (s0 + u < S)
         acc += sw[(s0 + u) * kRows + r] * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
   }
@@ -1023,9 +1034,10 @@ static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, h
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
   hipError_t e = launch_variant<D, BF16, true>(kp, pl, st);
   if (e != hipSuccess) return e;
-  constexpr int kRows = 256 / (D / 8);
+  constexpr int kRows = kCombineThreads / (D / 8);
   const int64_t blocks = (cp.rows + kRows - 1) / kRows;
-  hipLaunchKernelGGL((fa_combine_kernel<D, BF16>), dim3((unsigned)blocks), dim3(256), 0, st, cp);
+  hipLaunchKernelGGL((fa_combine_kernel<D, BF16>), dim3((unsigned)blocks), dim3(kCombineThreads),
+                     0, st, cp);
   return hipGetLastError();
 }
 
