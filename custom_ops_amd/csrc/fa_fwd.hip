@@ -741,34 +741,25 @@ struct CParams {
   int64_t rows;  // B*H*Sq
 };
 
-// Workgroup = one wave = kRows rows × D columns (4 rows for d = 128), so even
-// a small split grid gives hundreds of workgroups; thread = 8 consecutive
-// d-values of a row (one 16-byte load per split). Phase 1 stages the rows' LSEs in LDS and turns
+// Workgroup = kCombineThreads / (D/8) rows × D columns: 256 threads (16 rows
+// at d = 128) for large grids, one wave (4 rows) when that would leave fewer
+// than 1024 workgroups, so a small split grid still fills the chip; thread = 8
+// consecutive d-values of a row (one 16-byte load per split). Phase 1 stages the rows' LSEs in LDS and turns
 // them into weights w_s = exp(lse_s − max) / Σ (all-(-inf) row → all weights
-// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 16 splits'
-// loads in flight, the first 16 issued before phase 1.
-constexpr int kCombineThreads = 64;
-template <int D, bool BF16>
+// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 8 splits'
+// loads in flight. (Issuing them before phase 1 is slower: loads complete in
+// order, so the LSE reads would wait behind them.)
+template <int D, bool BF16, int kCombineThreads>
 __global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CParams p) {
   typedef typename Elt<BF16>::v8 V8;
   constexpr int kTPR = D / 8;                     // threads per row
   constexpr int kRows = kCombineThreads / kTPR;   // rows per workgroup
-  constexpr int kBatch = 16;                      // splits' loads in flight per thread
+  constexpr int kBatch = 8;                       // splits' loads in flight per thread
   __shared__ float sw[kMaxSplits * kRows];
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
   const int64_t slab = p.rows;
   const int S = p.num_splits;
-  const int r = tid / kTPR;
-  const int c8 = tid % kTPR;
-  const int64_t row = row0 + r;
-  const bool live = row < p.rows;
-  const uint16_t* src = p.o_part + row * D + c8 * 8;
-  // The first batch of partial rows is requested before the LSE round trip.
-  u32x4 raw[kBatch];
-#pragma unroll
-  for (int u = 0; u < kBatch; ++u)
-    if (live && u < S) raw[u] = *reinterpret_cast<const u32x4*>(src + (int64_t)u * slab * D);
   for (int i = tid; i < S * kRows; i += kCombineThreads) {
     const int s = i / kRows, rr = i % kRows;
     const int64_t lrow = row0 + rr;
@@ -789,12 +780,14 @@ __global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CPara
     for (int s = 0; s < S; ++s) sw[s * kRows + tid] *= inv;
   }
   __syncthreads();
-  if (!live) return;
+  const int r = tid / kTPR;
+  const int c8 = tid % kTPR;
+  const int64_t row = row0 + r;
+  if (row >= p.rows) return;
+  const uint16_t* src = p.o_part + row * D + c8 * 8;
   f32x8 acc = {};
-#pragma unroll
-  for (int u = 0; u < kBatch; ++u)
-    if (u < S) acc += sw[u * kRows + r] * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
-  for (int s0 = kBatch; s0 < S; s0 += kBatch) {
+  for (int s0 = 0; s0 < S; s0 += kBatch) {
+    u32x4 raw[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
       if (s0 + u < S) raw[u] = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + u) * slab * D);
@@ -1034,10 +1027,15 @@ static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, h
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
   hipError_t e = launch_variant<D, BF16, true>(kp, pl, st);
   if (e != hipSuccess) return e;
-  constexpr int kRows = kCombineThreads / (D / 8);
-  const int64_t blocks = (cp.rows + kRows - 1) / kRows;
-  hipLaunchKernelGGL((fa_combine_kernel<D, BF16>), dim3((unsigned)blocks), dim3(kCombineThreads),
-                     0, st, cp);
+  // 256-thread workgroups while they still number >= 1024, else one wave each.
+  constexpr int kRows256 = 256 / (D / 8), kRows64 = 64 / (D / 8);
+  if ((cp.rows + kRows256 - 1) / kRows256 >= 1024) {
+    hipLaunchKernelGGL((fa_combine_kernel<D, BF16, 256>),
+                       dim3((unsigned)((cp.rows + kRows256 - 1) / kRows256)), dim3(256), 0, st, cp);
+  } else {
+    hipLaunchKernelGGL((fa_combine_kernel<D, BF16, 64>),
+                       dim3((unsigned)((cp.rows + kRows64 - 1) / kRows64)), dim3(64), 0, st, cp);
+  }
   return hipGetLastError();
 }
 
