@@ -116,7 +116,10 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // The same buffer descriptor as make_rsrc, as four plain words for the asm.
 __device__ __forceinline__ i32x4 make_rsrc_words(const void* base, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)bytes, kRsrcFlags};
+  // Uniform by construction; readfirstlane makes the compiler keep it in SGPRs.
+  return i32x4{(int)__builtin_amdgcn_readfirstlane((uint32_t)a),
+               (int)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+               (int)__builtin_amdgcn_readfirstlane(bytes), kRsrcFlags};
 }
 // LDS byte address of a __shared__ array (folds to a constant after inlining).
 __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
@@ -656,7 +659,7 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
   typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
   constexpr int NST = WAVES == 8 ? MI355_FA_STAGES8 : MI355_FA_STAGES4;
-  static_assert(NST == 2 || NST == 3, "two or three stages");
+  static_assert(NST >= 2 && NST <= 4, "two to four stages");
   __shared__ __align__(16) uint16_t sK[NST][G::kKElems];
   __shared__ __align__(16) uint16_t sV[NST][G::kVElems];
   __shared__ __align__(16) uint16_t sM[G::kMElems];
@@ -711,21 +714,25 @@ __global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
       a.mask_init(sM);
     }
   };
+  // Unrolled by NST so every stage index is a compile-time constant; the
+  // remainder runs stages 0, 1, ... in order.
+  typedef std::integral_constant<int, 0> S0;
+  typedef std::integral_constant<int, 1> S1;
+  typedef std::integral_constant<int, 2> S2;
+  typedef std::integral_constant<int, 3> S3;
   int n = nb;
-  if constexpr (NST == 2) {
-    for (; n + 1 < ne; n += 2) {
-      iter(std::integral_constant<int, 0>{}, n);
-      iter(std::integral_constant<int, 1>{}, n + 1);
-    }
-    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
-  } else {
-    for (; n + 2 < ne; n += 3) {
-      iter(std::integral_constant<int, 0>{}, n);
-      iter(std::integral_constant<int, 1>{}, n + 1);
-      iter(std::integral_constant<int, 2>{}, n + 2);
-    }
-    if (n < ne) iter(std::integral_constant<int, 0>{}, n);
-    if (n + 1 < ne) iter(std::integral_constant<int, 1>{}, n + 1);
+  for (; n + NST - 1 < ne; n += NST) {
+    iter(S0{}, n);
+    iter(S1{}, n + 1);
+    if constexpr (NST > 2) iter(S2{}, n + 2);
+    if constexpr (NST > 3) iter(S3{}, n + 3);
+  }
+  if (n < ne) iter(S0{}, n);
+  if constexpr (NST > 2) {
+    if (n + 1 < ne) iter(S1{}, n + 1);
+  }
+  if constexpr (NST > 3) {
+    if (n + 2 < ne) iter(S2{}, n + 2);
   }
 
   a.epilogue(ti.b, ti.h, ti.split, qrow);
