@@ -652,10 +652,13 @@ struct Attn {
 #define MI355_FA_STAGES8 2
 #endif
 #ifndef MI355_FA_STAGES4
-#define MI355_FA_STAGES4 3
+#define MI355_FA_STAGES4 2
 #endif
+// Two waves per SIMD: the 8-wave workgroup alone, or two 4-wave workgroups
+// (80 KiB of LDS each at two stages) sharing a CU.
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void fa_fwd_kernel(const KParams p) {
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
   typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
   constexpr int NST = WAVES == 8 ? MI355_FA_STAGES8 : MI355_FA_STAGES4;
@@ -903,10 +906,10 @@ struct Plan {
 // fills the chip with whole rounds of workgroups. 8 waves (BM = 256, two
 // waves per SIMD) beat 4 when the 256-row tiles are mostly real rows and
 // each split keeps >= 16 KV tiles; the split count is then chosen so the
-// grid is one round of CUs. Otherwise 4 waves (BM = 128), with two rounds for
-// d = 64 (its KV tiles are half the bytes, so more workgroups are needed to
-// keep HBM busy) and one for d = 128. Every split keeps >= 4 KV tiles, so the
-// partial write and combine stay small next to the split's own work.
+// grid is one round of CUs. Otherwise 4 waves (BM = 128), two workgroups per
+// CU, with the split count chosen so the grid is one round of both slots
+// (2 x CUs workgroups). Every split keeps >= 4 KV tiles, so the partial write
+// and combine stay small next to the split's own work.
 static int fill_splits(int tiles, int rounds, int num_n, int cus) {
   int s = (int)lrintf((float)rounds * cus / (float)tiles);
   const int max_s = num_n / 4 > 1 ? num_n / 4 : 1;
@@ -932,7 +935,7 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
       if (s <= 0) s = s8;
     }
   }
-  if (s <= 0) s = fill_splits(bh * m128, p->d == 64 ? 2 : 1, pl.num_n, cus);
+  if (s <= 0) s = fill_splits(bh * m128, 2, pl.num_n, cus);
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > pl.num_n) s = pl.num_n;
   if (s < 1) s = 1;
