@@ -756,15 +756,18 @@ struct CParams {
 // than 1024 workgroups, so a small split grid still fills the chip; thread = 8
 // consecutive d-values of a row (one 16-byte load per split). Phase 1 stages the rows' LSEs in LDS and turns
 // them into weights w_s = exp(lse_s − max) / Σ (all-(-inf) row → all weights
-// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 8 splits'
-// loads in flight. (Issuing them before phase 1 is slower: loads complete in
+// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 32 (one
+// wave) or 8 (256 threads) splits' loads in flight. (Issuing them before phase 1 is slower: loads complete in
 // order, so the LSE reads would wait behind them.)
 template <int D, bool BF16, int kCombineThreads>
 __global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CParams p) {
   typedef typename Elt<BF16>::v8 V8;
   constexpr int kTPR = D / 8;                     // threads per row
   constexpr int kRows = kCombineThreads / kTPR;   // rows per workgroup
-  constexpr int kBatch = 8;                       // splits' loads in flight per thread
+  // splits' loads in flight per thread: all of a typical small grid's splits
+  // in one round trip for the one-wave variant; 8 keeps the large-grid
+  // variant's registers (and occupancy) low
+  constexpr int kBatch = kCombineThreads == 64 ? 32 : 8;
   __shared__ float sw[kMaxSplits * kRows];
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
@@ -906,10 +909,11 @@ struct Plan {
 // fills the chip with whole rounds of workgroups. 8 waves (BM = 256, two
 // waves per SIMD) beat 4 when the 256-row tiles are mostly real rows and
 // each split keeps >= 16 KV tiles; the split count is then chosen so the
-// grid is one round of CUs. Otherwise 4 waves (BM = 128), two workgroups per
-// CU, with the split count chosen so the grid is one round of both slots
-// (2 x CUs workgroups). Every split keeps >= 4 KV tiles, so the partial write
-// and combine stay small next to the split's own work.
+// grid is one round of CUs. Otherwise 4 waves (BM = 128): two rounds of CUs
+// for d = 64, one for d = 128 (two d = 128 workgroups can share a CU, but
+// filling both slots doubles the partials and measured slower with cold
+// caches). Every split keeps >= 4 KV tiles, so the partial write and combine
+// stay small next to the split's own work.
 static int fill_splits(int tiles, int rounds, int num_n, int cus) {
   int s = (int)lrintf((float)rounds * cus / (float)tiles);
   const int max_s = num_n / 4 > 1 ? num_n / 4 : 1;
@@ -935,7 +939,7 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
       if (s <= 0) s = s8;
     }
   }
-  if (s <= 0) s = fill_splits(bh * m128, 2, pl.num_n, cus);
+  if (s <= 0) s = fill_splits(bh * m128, p->d == 64 ? 2 : 1, pl.num_n, cus);
   if (s > kMaxSplits) s = kMaxSplits;
   if (s > pl.num_n) s = pl.num_n;
   if (s < 1) s = 1;

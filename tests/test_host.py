@@ -119,19 +119,19 @@ def test_cost_model_and_workspace(lib):
 
 @pytest.mark.parametrize("b,h,sq,sk,d,splits", [
     (4, 16, 2048, 2048, 128, 1),      # grid of 256-row tiles already fills 256 CUs
-    (1, 16, 128, 32768, 128, 32),     # 16 tiles of 128 rows, two per CU -> 512 workgroups
+    (1, 16, 128, 32768, 128, 16),     # 16 tiles of 128 rows -> one round of 256
     (2, 16, 1000, 4099, 128, 2),      # 128 tiles of 256 rows -> 2 splits
     (1, 16, 512, 32768, 128, 8),      # 32 tiles of 256 rows -> 8 splits
-    (1, 64, 1, 32768, 64, 8),         # decode: 64 tiles of 128 rows, two per CU
+    (1, 64, 1, 32768, 64, 8),         # d=64 decode: two rounds of 128-row tiles
     (1, 4, 512, 32768, 128, 32),
-    (1, 4, 512, 8192, 128, 32),       # 8 waves would leave 4 KV tiles a split: 4 waves
+    (1, 4, 512, 8192, 128, 16),       # 8 waves would leave 4 KV tiles a split: 4 waves
     (1, 1, 1, 256, 128, 1),           # >= 4 KV tiles per split caps the count
     (1, 1, 1, 1024, 128, 4),
 ])
 def test_auto_plan_fills_whole_rounds(lib, b, h, sq, sk, d, splits):
     """The launcher's own plan on a 256-CU part (no GPU here: the library
-    assumes 256 CUs when none can be queried): 8 waves with one workgroup per
-    CU, else 4 waves with two per CU, splits filling one round of slots."""
+    assumes 256 CUs when none can be queried): 8 waves with one round of
+    workgroups, else 4 waves with two rounds (d = 64) or one (d = 128)."""
     from custom_ops_amd import _lib
     p = _params(b=b, h=h, h_k=h, seqlen_q=sq, seqlen_k=sk, d=d, mask_seqlen_q=sq,
                 mask_seqlen_k=sk, q_row_stride=d, k_row_stride=d, v_row_stride=d,
