@@ -154,6 +154,16 @@ def cpu_configs(seconds_each):
                      "tflops": round(c.flops / (us_full * 1e-6) / 1e12, 5),
                      "heads_timed": f"{done}/{len(heads)}",
                      "extrapolated": done < len(heads)}
+    # cfg1 also through the build's C restatement (one thread, fp32, the
+    # reference kernel's tile-wise online softmax), whole.
+    from oracle.oracle import oracle_fwd
+    c = CONFIGS["cfg1"]
+    q, k, v, m = (t.float().numpy() for t in make_inputs(c))
+    t0 = time.perf_counter()
+    oracle_fwd(q, k, v, m, dtype="fp32", block_n=64)
+    el = time.perf_counter() - t0
+    out["cfg1"]["c_restatement_us"] = round(el * 1e6, 1)
+    out["cfg1"]["c_restatement_threads"] = 1
     return out
 
 
