@@ -756,8 +756,8 @@ struct CParams {
 // than 1024 workgroups, so a small split grid still fills the chip; thread = 8
 // consecutive d-values of a row (one 16-byte load per split). Phase 1 stages the rows' LSEs in LDS and turns
 // them into weights w_s = exp(lse_s − max) / Σ (all-(-inf) row → all weights
-// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 32 (one
-// wave) or 8 (256 threads) splits' loads in flight. (Issuing them before phase 1 is slower: loads complete in
+// 0 → output 0); phase 2 accumulates Σ w_s·O_s in fp32 with up to 16 (one
+// wave) or 8 (256 threads) splits' loads in flight (more spills SGPRs). (Issuing them before phase 1 is slower: loads complete in
 // order, so the LSE reads would wait behind them.)
 template <int D, bool BF16, int kCombineThreads>
 __global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CParams p) {
@@ -767,7 +767,7 @@ __global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CPara
   // splits' loads in flight per thread: all of a typical small grid's splits
   // in one round trip for the one-wave variant; 8 keeps the large-grid
   // variant's registers (and occupancy) low
-  constexpr int kBatch = kCombineThreads == 64 ? 32 : 8;
+  constexpr int kBatch = kCombineThreads == 64 ? 16 : 8;
   __shared__ float sw[kMaxSplits * kRows];
   const int tid = threadIdx.x;
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
