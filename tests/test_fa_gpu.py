@@ -363,6 +363,54 @@ def test_vs_c_oracle_small(ops, gpu):
         assert torch.all(out[:, :, 3] == 0)
 
 
+
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_finfo_min_masks(ops, gpu, dtype, name, splits):
+    """Masks built the Hugging Face way, with torch.finfo(dtype).min as
+    "blocked". The reference kernel adds mask·(1/scale) to the unscaled scores
+    in fp32 (csrc/fa/sm89/fa_fwd_kernel.h:286-310): for bf16 that overflows to
+    -inf, so a row of minima is fully masked and exactly 0; for fp16 it stays
+    finite, so a row of minima is an ordinary softmax over q·k. The C oracle
+    restates that arithmetic."""
+    from custom_ops_amd import mha_fwd_with_mask
+    from oracle import oracle as orc
+    q, k, v, _ = make_case(2, 4, 2, 80, 200, 128, "zero", dtype, seed=11)
+    g = torch.Generator().manual_seed(5)
+    lo = torch.finfo(dtype).min
+    m = torch.zeros(2, 1, 80, 200).masked_fill(torch.rand(2, 1, 80, 200, generator=g) < 0.3, lo)
+    m[:, :, 5, :] = lo
+    m[:, :, 6, :] = float("-inf")
+    m = m.to(dtype)
+    out = mha_fwd_with_mask(q.to(gpu), k.to(gpu), v.to(gpu), m.to(gpu), num_splits=splits).cpu()
+    ref = torch.from_numpy(orc.oracle_fwd(q.float().numpy(), k.float().numpy(),
+                                          v.float().numpy(), m.float().numpy(), dtype=name))
+    assert_close(out, ref, f"finfo-min-{name}-s{splits}")
+    assert torch.all(out[:, :, 6] == 0)
+    if dtype == torch.bfloat16:
+        assert torch.all(out[:, :, 5] == 0)
+    else:
+        assert torch.all(torch.isfinite(out[:, :, 5].float())) and out[:, :, 5].abs().sum() > 0
+
+
+
+@pytest.mark.parametrize("slope", [0.2, -0.2, 0.02])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_moving_running_max(ops, gpu, slope, splits):
+    """A mask bias that rises along the keys moves the running max on every
+    64-key tile (0.2 per key = 12.8 per tile, past the lazy-rescale slack each
+    time), a falling one never moves it after the first tile, a gentle one
+    moves it every few tiles; logits reach about +-200."""
+    from custom_ops_amd import mha_fwd_with_mask
+    for dtype in (torch.bfloat16, torch.float16):
+        q, k, v, _ = make_case(1, 2, 2, 64, 1024, 128, "zero", dtype, seed=3)
+        ramp = (torch.arange(1024, dtype=torch.float32) * slope).view(1, 1, 1, -1)
+        m = ramp.expand(1, 1, 64, 1024).contiguous().to(dtype)
+        out = mha_fwd_with_mask(q.to(gpu), k.to(gpu), v.to(gpu), m.to(gpu), num_splits=splits)
+        ref = ref_attn_torch(q.to(gpu), k.to(gpu), v.to(gpu), m.to(gpu))
+        assert_close(out, ref, f"ramp{slope}-s{splits}-{dtype}")
+
+
 def test_golden_fixtures(ops, gpu):
     from tests.golden import load_fixtures
     for fx in load_fixtures():
