@@ -27,8 +27,11 @@
 //   * The widened, pre-scaled mask tile initialises the QK accumulators, so no
 //     pass over the scores sits between the two GEMMs except the row max.
 //   * K, V and the mask tile of tile n+1 go HBM → LDS by buffer_load ... lds
-//     (no VGPR staging) while tile n computes; double-buffered LDS, one barrier
-//     per tile. XOR swizzles keep every LDS read conflict-free.
+//     (no VGPR staging, issued as inline assembly with explicit waits) while
+//     tile n computes; two K/V stages, one barrier per tile. Each wave loads
+//     its own 32 mask rows into a single buffer and widens the next tile's mask
+//     before the barrier. XOR swizzles keep every LDS read conflict-free.
+//   * Two waves per SIMD: one 8-wave workgroup, or two 4-wave workgroups, per CU.
 //   * Lazy rescaling: the running max moves only when a score exceeds it by
 //     more than 8 (log2 units); O and l are rescaled on those tiles only.
 //   * Sk tails are predicated in-kernel (buffer-resource bounds return 0 for
