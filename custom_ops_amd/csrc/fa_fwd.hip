@@ -283,9 +283,10 @@ __device__ __forceinline__ TileIdx tile_index(const KParams& p) {
 }
 
 // ── main kernel: 32 query rows per wave, WAVES = 4 or 8 waves ─────────────────
-// A wave needs ~250 registers; with 8 waves (BM = 256) two waves share every
-// SIMD, hiding each other's LDS and MFMA latencies. 4 waves (BM = 128) serve
-// small grids and split-KV. K, V and the mask tile arrive by LDS DMA; V is read transposed.
+// A wave needs 210-245 registers (two waves per SIMD fit); with 8 waves
+// (BM = 256) two waves share every SIMD, hiding each other's LDS and MFMA
+// latencies. 4 waves (BM = 128) serve small grids and split-KV. K, V and the
+// mask tile arrive by LDS DMA; V is read transposed.
 //  sK   [kBN][D]    unit c of row r at slot c ^ (r % UPR)   (π-permuted rows)
 //  sM   [BM][kBN]   unit u of row m at slot u ^ ((m/2) % 8)
 //  sV   [kBN][D]    natural key order, unit c of row r at slot c ^ swzV(r); the
@@ -650,7 +651,8 @@ struct Attn {
 // LDS buffer and no barrier, and the next tile's GEMM starts right after the
 // barrier. Aligned rows arrive by LDS DMA; unaligned rows go through registers
 // (element-wise past Sk) and the wave stores them to its rows of the buffer.
-// Measured and not kept: skipping all -inf mask blocks, persistent workgroups.
+// Measured and not kept: skipping all -inf mask blocks, persistent workgroups
+// with cross-item prefetch, a software-pipelined softmax(n) / PV(n-1) loop.
 #ifndef MI355_FA_STAGES8
 #define MI355_FA_STAGES8 2
 #endif
