@@ -411,6 +411,39 @@ def test_moving_running_max(ops, gpu, slope, splits):
         assert_close(out, ref, f"ramp{slope}-s{splits}-{dtype}")
 
 
+
+@pytest.mark.parametrize("shape,splits", [((1, 4, 2, 200, 3000, 128), 0),   # auto: split
+                                          ((2, 4, 4, 300, 700, 64), 1)])   # unsplit
+def test_graph_capture_replays(ops, gpu, shape, splits):
+    """The op captured in a HIP graph (workspace from the graph-aware caching
+    allocator, no memset nodes) and replayed several times with new inputs
+    copied into the captured buffers, eager work and synchronisations in
+    between: every replay equals the eager result bit for bit."""
+    from custom_ops_amd import mha_fwd_with_mask
+    b, h, hk, sq, sk, d = shape
+    q, k, v, m = (t.to(gpu) for t in make_case(b, h, hk, sq, sk, d, "inf_random",
+                                              torch.bfloat16, seed=21))
+    fn = lambda: mha_fwd_with_mask(q, k, v, m, num_splits=splits)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    for seed in (1, 2, 3):
+        nq, nk, nv, nm = (t.to(gpu) for t in make_case(b, h, hk, sq, sk, d, "inf_random",
+                                                      torch.bfloat16, seed=seed))
+        q.copy_(nq); k.copy_(nk); v.copy_(nv); m.copy_(nm)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = fn()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay with seed {seed}"
+
+
 def test_golden_fixtures(ops, gpu):
     from tests.golden import load_fixtures
     for fx in load_fixtures():
