@@ -275,6 +275,42 @@ def test_random_shape_sweep(ops, gpu, case):
     assert torch.all(out.permute(0, 2, 1, 3)[rows_dead.to(gpu)] == 0)
 
 
+
+def _sweep_cases_large(n=24, seed=77):
+    """Larger seeded shapes: several 256-row blocks (both tile orders), long Sk
+    with automatic splits, GQA up to 8:1, forced workgroup sizes."""
+    import random
+    rnd = random.Random(seed)
+    kinds = ["zero", "causal", "random", "inf_random", "bias", "full_row", "block"]
+    cases = []
+    while len(cases) < n:
+        d = rnd.choice([64, 128])
+        hk = rnd.choice([1, 2, 4, 8])
+        h = hk * rnd.choice([1, 2, 4, 8])
+        b = rnd.choice([1, 2])
+        sq = rnd.choice([300, 511, 700, 1024, 1100])
+        sk = rnd.choice([2049, 4096, 5000, 9001])
+        if b * h * sq * sk > 5e7:
+            continue
+        cases.append((len(cases), b, h, hk, sq, sk, d, rnd.choice(["bf16", "fp16"]),
+                      rnd.choice(kinds), rnd.choice([(0, 0), (0, 0), (5, 3)]),
+                      rnd.choice([0, 0, 0, 3]), rnd.choice(["", "", "4", "8"])))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases_large(), ids=lambda c: f"large{c[0]}")
+def test_random_shape_sweep_large(ops, gpu, monkeypatch, case):
+    i, b, h, hk, sq, sk, d, dtype, kind, (pad_r, pad_c), splits, waves = case
+    if waves:
+        monkeypatch.setenv("MI355_FA_WAVES", waves)
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    c = make_case(b, h, hk, sq, sk, d, kind, dt, seed=5000 + i, extra_rows=pad_r,
+                  extra_cols=pad_c)
+    out, _ = run(ops, c, gpu, f"large{i} {case[1:]}", num_splits=splits)
+    rows_dead = torch.isinf(c[3][:, 0, :sq, :sk].float()).all(-1)
+    assert torch.all(out.permute(0, 2, 1, 3)[rows_dead.to(gpu)] == 0)
+
+
 def test_all_masked_everything_split(ops, gpu):
     q, k, v, m = make_case(1, 2, 2, 64, 4096, 128, "zero", torch.bfloat16)
     m = torch.full_like(m, float("-inf"))
