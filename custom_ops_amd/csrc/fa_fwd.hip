@@ -526,20 +526,24 @@ struct Attn {
 
   // softmax of tile n and Oᵀ += Vᵀ·Pᵀ, the exponentials of each key step one
   // step ahead of its MFMAs
+  // A tile in which no row of the wave has a live key (every score -inf, e.g.
+  // outside a sliding window) contributes P = 0 exactly: l and O stay as they
+  // are bit for bit, so its exponentials and PV product are skipped.
   __device__ __forceinline__ void softmax_pv(const uint16_t* sVt) {
-    rescale(s);
-    exp_pv(sVt, s);
+    if (rescale(s)) exp_pv(sVt, s);
   }
 
   // row max of a tile's scores; moves the running max (and rescales O, l)
-  // only when it grew by more than the slack
-  __device__ __forceinline__ void rescale(const Scores& sc) {
+  // only when it grew by more than the slack. Returns whether any row of the
+  // wave has a key that is not -inf in this tile (NaN counts as live).
+  __device__ __forceinline__ bool rescale(const Scores& sc) {
     float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < NKB; ++b)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[b][i]);
     mx = xhalf_max(mx);
+    const bool live = __builtin_amdgcn_ballot_w64(!(mx == -INFINITY)) != 0;
     const bool need = mx > m_run + slack_u;
     if (__builtin_amdgcn_ballot_w64(need)) {
       // lanes that keep their max scale by exactly 1 (also avoids -inf - -inf)
@@ -550,6 +554,7 @@ struct Attn {
 #pragma unroll
       for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
     }
+    return live;
   }
 
   // P = exp2(u·c2 − m_run·c2) rounded to the input dtype; l += Σ P; Oᵀ += Vᵀ·Pᵀ

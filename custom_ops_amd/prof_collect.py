@@ -106,6 +106,7 @@ def main() -> None:
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "profiles"))
     args = ap.parse_args()
+    args.out = os.path.abspath(args.out)      # the passes run with cwd=/tmp
     os.makedirs(args.out, exist_ok=True)
     sys.path.insert(0, ROOT)
     from custom_ops_amd.workloads import CONFIGS

@@ -220,21 +220,23 @@ def _skip_mask(kind, b, sq, sk, g):
 @pytest.mark.parametrize("kind", ["causal", "window", "dead_stripes", "pad_rows_cols"])
 @pytest.mark.parametrize("waves", ["4", "8"])
 @pytest.mark.parametrize("splits", [1, 3])
-def test_dead_mask_blocks(ops, gpu, monkeypatch, kind, waves, splits):
-    """Masks with whole 32-row x 64-key blocks at -inf (a wave skips the QK /
-    softmax / PV work of such a tile): results match the fp32 reference, and
-    rows that see no key are exactly 0."""
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 64)],
+                         ids=["bf16d128", "fp16d64"])
+def test_dead_mask_blocks(ops, gpu, monkeypatch, kind, waves, splits, dtype, d):
+    """Masks with whole 32-row x 64-key blocks at -inf (a wave skips the
+    softmax / PV work of a tile in which none of its rows sees a key): results
+    match the fp32 reference, and rows that see no key are exactly 0."""
     from custom_ops_amd import mha_fwd_with_mask
     monkeypatch.setenv("MI355_FA_WAVES", waves)
     g = torch.Generator().manual_seed(7)
-    b, h, hk, sq, sk, d = 2, 4, 2, 700, 1500, 128
-    q = _rand((b, h, sq, d), g).to(torch.bfloat16).to(gpu)
-    k = _rand((b, hk, sk, d), g).to(torch.bfloat16).to(gpu)
-    v = _rand((b, hk, sk, d), g).to(torch.bfloat16).to(gpu)
-    m = _skip_mask(kind, b, sq, sk, g).to(torch.bfloat16).to(gpu)
+    b, h, hk, sq, sk = 2, 4, 2, 700, 1500
+    q = _rand((b, h, sq, d), g).to(dtype).to(gpu)
+    k = _rand((b, hk, sk, d), g).to(dtype).to(gpu)
+    v = _rand((b, hk, sk, d), g).to(dtype).to(gpu)
+    m = _skip_mask(kind, b, sq, sk, g).to(dtype).to(gpu)
     out = mha_fwd_with_mask(q, k, v, m, num_splits=splits)
     torch.cuda.synchronize()
-    assert_close(out, ref_attn_torch(q, k, v, m), f"dead blocks {kind} w{waves} s{splits}")
+    assert_close(out, ref_attn_torch(q, k, v, m), f"dead blocks {kind} w{waves} s{splits} d{d}")
     dead_rows = torch.isinf(m).all(-1).squeeze(1)          # [b, sq]
     assert torch.all(out.permute(0, 2, 1, 3)[dead_rows] == 0)
 
