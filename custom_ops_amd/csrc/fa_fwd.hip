@@ -592,54 +592,62 @@ struct Attn {
     }
   }
 
-  __device__ __forceinline__ void epilogue(int b, int h, int split, int qrow) {
+  // O (or a split's partial O) of the wave's 32 rows, normalised by l and
+  // rounded to the input dtype, leaves through LDS. In the MFMA layout a lane
+  // holds 4 consecutive d of one row per 16-byte chunk, so a direct store
+  // instruction would touch 32 rows with 8 bytes each; re-read from LDS, a
+  // lane holds one whole 16-byte chunk and a store instruction writes
+  // 64 / (D/8) consecutive whole rows. Chunks are XOR-swizzled by row so the
+  // writes and re-reads are free of bank conflicts. stg is this wave's own
+  // 32·D·2-byte LDS region, which no other wave touches.
+  __device__ __forceinline__ void epilogue(int b, int h, int split, int qrow, uint8_t* stg) {
     const float l = xhalf_sum(l_run);
     const float inv = (l == 0.f || l != l) ? 1.f : 1.f / l;
+    constexpr int CH = D / 8;      // 16-byte chunks per row
+    constexpr int RPI = 64 / CH;   // rows per re-read instruction
+    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+    typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        f32x4 v4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
+        u32x2 packed;
+        if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
+        else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
+        const int c = db * 4 + q4;   // chunk of d = db·32 + q4·8 .. +7; this lane's half g
+        *reinterpret_cast<u32x2*>(stg + l32 * D * 2 + ((c ^ (l32 & (CH - 1))) * 16) + g * 8) = packed;
+      }
+    }
+    const int ch = lane % CH, r0 = lane / CH;
+    const int row0 = qrow - l32;   // the wave's first row
     if constexpr (!SPLIT) {
       const rsrc_t ro = make_rsrc(p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs,
                                   (uint32_t)p.sq * p.o_rs * 2u);
-      const uint32_t obase = (uint32_t)(qrow * p.o_rs + g * 4) * 2u;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          f32x4 v4;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
-          typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-          typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
-          u32x2 packed;
-          if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
-          else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
-          __builtin_amdgcn_raw_buffer_store_b64(packed, ro, obase + (db * 32 + q4 * 8) * 2u, 0, 0);
-        }
+      for (int k = 0; k < 32 / RPI; ++k) {
+        const int r = r0 + k * RPI;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
+        // rows at or past Sq fall outside the buffer and are dropped
+        __builtin_amdgcn_raw_buffer_store_b128(v, ro, (uint32_t)((row0 + r) * p.o_rs + ch * 8) * 2u, 0, 0);
       }
     } else {
-      if (qrow >= p.sq) return;
-      const int64_t bh = (int64_t)b * p.h + h;
-      const int64_t slab = (int64_t)p.b * p.h * p.sq;
-      const int64_t prow = (int64_t)split * slab + bh * p.sq + qrow;
       // partial O normalised by the split's own l, rounded to the input
       // dtype as the reference stores it (fa_fwd_launch.h:289-297)
-      uint16_t* op = p.o_part + prow * D;
+      const int64_t bh = (int64_t)b * p.h + h;
+      const int64_t slab = (int64_t)p.b * p.h * p.sq;
+      const int64_t pbase = (int64_t)split * slab + bh * p.sq;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          f32x4 v4;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
-          typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-          typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
-          u32x2 packed;
-          if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
-          else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
-          *reinterpret_cast<u32x2*>(op + db * 32 + q4 * 8 + g * 4) = packed;
-        }
+      for (int k = 0; k < 32 / RPI; ++k) {
+        const int r = r0 + k * RPI;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
+        if (row0 + r < p.sq) *reinterpret_cast<u32x4*>(p.o_part + (pbase + row0 + r) * D + ch * 8) = v;
       }
-      if (g == 0)
-        p.lse_part[prow] = (l == 0.f || l != l) ? -INFINITY
-                                                 : __builtin_fmaf(m_run, p.scale, __builtin_amdgcn_logf(l) * 0.69314718f);
+      if (g == 0 && qrow < p.sq)
+        p.lse_part[pbase + qrow] = (l == 0.f || l != l) ? -INFINITY
+                                   : __builtin_fmaf(m_run, p.scale, __builtin_amdgcn_logf(l) * 0.69314718f);
     }
   }
 };
@@ -748,7 +756,15 @@ void fa_fwd_kernel(const KParams p) {
     if (n + 2 < ne) iter(S2{}, n + 2);
   }
 
-  a.epilogue(ti.b, ti.h, ti.split, qrow);
+  // The K/V stages are free once every wave is past its last tile (and no
+  // DMA is in flight): each wave stages its output rows in a private slice.
+  static_assert(4 * 32 * D * 2 <= NST * G::kKElems * 2 && 4 * 32 * D * 2 <= NST * G::kVElems * 2,
+                "output staging fits in the K and V stages");
+  wait_vmcnt<0>();
+  wg_barrier();
+  uint8_t* stg = (a.wave < 4 ? reinterpret_cast<uint8_t*>(&sK[0][0]) : reinterpret_cast<uint8_t*>(&sV[0][0]))
+                 + (a.wave & 3) * 32 * D * 2;
+  a.epilogue(ti.b, ti.h, ti.split, qrow, stg);
 }
 
 // ── split-KV combine ────────────────────────────────────────────────────────
