@@ -930,50 +930,65 @@ struct Plan {
   size_t o_part_bytes, lse_bytes, ws_bytes;
 };
 
-// Tile plan. Measured on MI355X over small grids (bh 1..64, Sq 1..512,
-// Sk 2k..32k, d 64/128, every workgroup size × split count): the best plan
-// fills the chip with whole rounds of workgroups. 8 waves (BM = 256, two
-// waves per SIMD) beat 4 when the 256-row tiles are mostly real rows and
-// each split keeps >= 16 KV tiles; the split count is then chosen so the
-// grid is one round of CUs. Otherwise 4 waves (BM = 128): two rounds of CUs
-// for d = 64, one for d = 128 (two d = 128 workgroups can share a CU, but
-// filling both slots doubles the partials and measured slower with cold
-// caches). Every split keeps >= 4 KV tiles, so the partial write and combine
-// stay small next to the split's own work.
-static int fill_splits(int tiles, int rounds, int num_n, int cus) {
-  int s = (int)lrintf((float)rounds * cus / (float)tiles);
-  const int max_s = num_n / 4 > 1 ? num_n / 4 : 1;
-  if (s > max_s) s = max_s;
-  return s < 1 ? 1 : s;
+// Tile plan: the workgroup size (4 or 8 waves) and split count with the
+// lowest modelled launch time. The model prices the busiest CU, which runs
+// k = ceil(W / CUs) of the W workgroups: 8-wave workgroups (BM = 256) one
+// after another; 4-wave workgroups (BM = 128) two at a time (a CU holds
+// two), an odd last one alone and faster. Each workgroup costs a fixed part
+// plus a per-KV-tile part; a split launch adds the combine (a fixed part,
+// its partial bytes and the splits per row). The constants are least-squares
+// fits, on relative error, to hot back-to-back timings on MI355X with zero
+// masks: d = 128 over 98 shapes (bh 1..64, Sq 1..2048, Sk 1k..32k), d = 64
+// over 76, each with both workgroup sizes and 1..64 splits. Chosen that way,
+// the plans come within 1 % (d = 128) and 3 % (d = 64) of each shape's
+// measured best in total, where filling one round of CUs with 8-wave
+// workgroups, else with 4-wave ones, came within 5 % and 10 %. Every split
+// keeps >= 4 KV tiles.
+struct PlanCost { float t8, o8, t4pair, t4solo, o4, c0, c_mb, c_split; };
+constexpr PlanCost kCostD128 = {1.819f, 3.630f, 2.197f, 1.258f, 1.923f, 5.251f, 0.453f, 0.106f};
+constexpr PlanCost kCostD64 = {1.334f, 2.139f, 1.427f, 0.932f, 1.109f, 5.791f, 0.417f, 0.128f};
+
+static float plan_cost(const PlanCost& c, int bh, int sq, int num_n, int d, int waves, int s,
+                       int cus) {
+  const int64_t wgs = (int64_t)bh * ceil_div(sq, 32 * waves) * s;
+  const int64_t k = (wgs + cus - 1) / cus;   // workgroups on the busiest CU
+  const float nps = (float)ceil_div(num_n, s);
+  float t = waves == 8 ? (float)k * (nps * c.t8 + c.o8)
+                       : (float)(k / 2) * (nps * c.t4pair + c.o4) + (float)(k % 2) * (nps * c.t4solo + c.o4);
+  if (s > 1) t += c.c0 + c.c_mb * ((float)bh * sq * s * d * 2.f * 1e-6f) + c.c_split * (float)s;
+  return t;
 }
 
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
   pl.num_n = ceil_div(p->seqlen_k, kBN);
   const int bh = p->b * p->h;
-  int s = p->num_splits;
-  if (s <= 0) {
+  int s_fixed = p->num_splits;
+  if (s_fixed <= 0) {
     const char* env = getenv("MI355_FA_NUM_SPLITS");
-    if (env && atoi(env) > 0) s = atoi(env);
+    if (env && atoi(env) > 0) s_fixed = atoi(env);
   }
-  const int m256 = ceil_div(p->seqlen_q, 256), m128 = ceil_div(p->seqlen_q, 128);
-  pl.waves = 4;
-  if (p->seqlen_q >= 192 * m256) {
-    const int s8 = fill_splits(bh * m256, 1, pl.num_n, cus);
-    if (s8 == 1 || pl.num_n >= 16 * s8) {
-      pl.waves = 8;
-      if (s <= 0) s = s8;
-    }
-  }
-  if (s <= 0) s = fill_splits(bh * m128, p->d == 64 ? 2 : 1, pl.num_n, cus);
-  if (s > kMaxSplits) s = kMaxSplits;
-  if (s > pl.num_n) s = pl.num_n;
-  if (s < 1) s = 1;
-  pl.splits = s;
+  if (s_fixed > kMaxSplits) s_fixed = kMaxSplits;
+  if (s_fixed > pl.num_n) s_fixed = pl.num_n;
+  int w_fixed = 0;
   {   // tuning override of the workgroup size (4 or 8 waves)
     const char* w = getenv("MI355_FA_WAVES");
-    if (w && (atoi(w) == 4 || atoi(w) == 8)) pl.waves = atoi(w);
+    if (w && (atoi(w) == 4 || atoi(w) == 8)) w_fixed = atoi(w);
   }
+  const PlanCost& cm = p->d == 64 ? kCostD64 : kCostD128;
+  int max_s = pl.num_n / 4 > 1 ? pl.num_n / 4 : 1;
+  if (max_s > kMaxSplits) max_s = kMaxSplits;
+  float best = 0.f;
+  pl.waves = 0;
+  for (int w = 4; w <= 8; w += 4) {
+    if (w_fixed && w != w_fixed) continue;
+    for (int s = s_fixed > 0 ? s_fixed : 1; s <= (s_fixed > 0 ? s_fixed : max_s); ++s) {
+      const float c = plan_cost(cm, bh, p->seqlen_q, pl.num_n, p->d, w, s, cus);
+      if (pl.waves == 0 || c < best) { best = c; pl.waves = w; pl.splits = s; }
+    }
+  }
+  if (pl.splits < 1) pl.splits = 1;
+  const int s = pl.splits;
   pl.block_m = 32 * pl.waves;
   // Workgroup order. Each XCD runs a contiguous range of tile ids and has its
   // own L2. With few m-blocks per head, the mask tile (shared by all heads of
