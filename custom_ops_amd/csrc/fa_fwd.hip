@@ -664,8 +664,10 @@ struct Attn {
 // LDS buffer and no barrier, and the next tile's GEMM starts right after the
 // barrier. Aligned rows arrive by LDS DMA; unaligned rows go through registers
 // (element-wise past Sk) and the wave stores them to its rows of the buffer.
-// Measured and not kept: skipping all -inf mask blocks, persistent workgroups
-// with cross-item prefetch, a software-pipelined softmax(n) / PV(n-1) loop.
+// Measured and not kept: testing the mask block before QK to skip a whole
+// dead tile, persistent workgroups with cross-item prefetch, a software-
+// pipelined softmax(n) / PV(n-1) loop, 4 waves of 64 rows, a combine done by
+// each row block's last split (its device-scope release writes back the L2).
 #ifndef MI355_FA_STAGES8
 #define MI355_FA_STAGES8 2
 #endif
@@ -893,8 +895,8 @@ static int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // in the main kernel, P = per-split cost of the partial write + combine.
 // slots = workgroups resident per CU (cap_fill = slots·SMs / m-blocks; the
 // reference's kernel fits 2 per SM). Exported as mi355_fa_cost_model_splits
-// with the reference's constants; the launcher's own plan (make_plan) uses a
-// rule measured on MI355X instead.
+// with the reference's constants; the launcher's own plan (make_plan) uses an
+// occupancy cost model fitted to MI355X timings instead.
 static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int cus,
                              int slots = 2) {
   if (cus <= 0) cus = 1;
