@@ -694,12 +694,16 @@ void fa_fwd_kernel(const KParams p) {
   const rsrc_t rq = make_rsrc(p.q + (int64_t)ti.b * p.q_bs + (int64_t)ti.h * p.q_hs,
                               (uint32_t)p.sq * p.q_rs * 2u);
   const int qrow = ti.m0 + a.wave * 32 + a.l32;
-  // Zero the V buffers once: a V row the tail's DMA leaves unwritten then holds
-  // 0 or an earlier tile's finite values, and its P is 0, so it adds nothing.
-  for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads)
+  // With Sk % 64 != 0, zero the V buffers once: a V row the tail's DMA leaves
+  // unwritten then holds 0 or an earlier tile's finite values, and its P is 0,
+  // so it adds nothing. Whole tiles overwrite every row: no zeroing, and no
+  // barrier before the first DMAs.
+  if (p.sk % kBN != 0) {
+    for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads)
 #pragma unroll
-    for (int st = 0; st < NST; ++st) reinterpret_cast<u32x4*>(sV[st])[i] = u32x4{0u, 0u, 0u, 0u};
-  __syncthreads();
+      for (int st = 0; st < NST; ++st) reinterpret_cast<u32x4*>(sV[st])[i] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+  }
   const int cnt = ne - nb;
   if (cnt > 0) a.issue_m(nb, sM);
 #pragma unroll
