@@ -1049,12 +1049,12 @@ static int validate(const mi355_fa_params* p, char* err, size_t errlen) {
       set_err(err, errlen, "tensor pointer is NULL");
       return MI355_FA_EINVAL;
     }
-    // 16-byte vector access to q/k/v/o rows
+    // 16-byte vector access to q/k/v/o rows (O leaves in 16-byte row chunks)
     const uintptr_t al = (uintptr_t)p->q | (uintptr_t)p->o | (uintptr_t)p->k | (uintptr_t)p->v;
     const int64_t st = p->q_batch_stride | p->q_head_stride | p->q_row_stride | p->k_batch_stride |
                        p->k_head_stride | p->k_row_stride | p->v_batch_stride | p->v_head_stride |
-                       p->v_row_stride;
-    if ((al & 15) || (st & 7) || ((p->o_batch_stride | p->o_head_stride | p->o_row_stride) & 3)) {
+                       p->v_row_stride | p->o_batch_stride | p->o_head_stride | p->o_row_stride;
+    if ((al & 15) || (st & 7)) {
       set_err(err, errlen, "q/k/v/o must be 16-byte aligned with strides that are multiples of 8 elements");
       return MI355_FA_EINVAL;
     }

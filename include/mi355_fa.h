@@ -48,6 +48,8 @@ enum { MI355_FA_FP16 = 0, MI355_FA_BF16 = 1 };
  *   q    [B, H,  Sq, d]   o [B, H, Sq, d]
  *   k, v [B, Hk, Sk, d]   innermost (d) stride must be 1
  *   mask [B, 1, mask_seqlen_q >= Sq, mask_seqlen_k >= Sk], innermost stride 1
+ * q, k, v and o: 16-byte aligned base, every stride a multiple of 8 elements
+ * (rows move as 16-byte chunks); mask: 2-byte aligned, any strides.
  * Mask columns >= seqlen_k are always treated as blocked whatever they hold;
  * mask rows >= seqlen_q are never read for output. Sk need not be a multiple
  * of 8: the kernel predicates the K/V tail and reads unaligned mask rows

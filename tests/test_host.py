@@ -73,6 +73,7 @@ def _params(**kw):
     ("h_k", 3, "divisible by n_kv_heads"),
     ("h_k", 0, "divisible by n_kv_heads"),
     ("mask_seqlen_q", 100, "mask shape"),
+    ("o_row_stride", 132, "multiples of 8 elements"),   # O leaves in 16-byte row chunks
     ("mask_seqlen_k", 255, "mask shape"),
     ("scale_softmax", -1.0, "scale_softmax"),
     ("q", 0, "NULL"),
