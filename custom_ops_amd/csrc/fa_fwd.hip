@@ -557,7 +557,10 @@ struct Attn {
     return live;
   }
 
-  // P = exp2(u·c2 − m_run·c2) rounded to the input dtype; l += Σ P; Oᵀ += Vᵀ·Pᵀ
+  // P = exp2(u·c2 − m_run·c2) rounded to the input dtype; l += Σ P; Oᵀ += Vᵀ·Pᵀ.
+  // The exponentials of key step j + 1 are issued before the MFMAs of step j,
+  // so no MFMA waits on exponentials produced just before it (l accumulates
+  // the steps in order either way).
   __device__ __forceinline__ void exp_pv(const uint16_t* sVt, const Scores& sc) {
     // PV operands (step i: local key step j = i / DB of 8 keys, d block
     // db = i % DB) stream through a window of kWin LDS reads in flight.
@@ -574,21 +577,30 @@ struct Attn {
     V8 win[kWin];
 #pragma unroll
     for (int i = 0; i < kWin; ++i) win[i] = rd(i);
-    V8 pb;
+    auto pstep = [&](int j) {
+      f32x8 pf;
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int j = i / DB;
-      if (i % DB == 0) {
-        f32x8 pf;
+      for (int e = 0; e < 8; ++e)
+        pf[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j / 2][(j % 2) * 8 + e], c2, -mlog2));
+      return __builtin_convertvector(pf, V8);
+    };
+    V8 pcur = pstep(0);
+    l_run = psum8<BF16>(pcur, l_run);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          pf[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j / 2][(j % 2) * 8 + e], c2, -mlog2));
-        pb = __builtin_convertvector(pf, V8);
-        l_run = psum8<BF16>(pb, l_run);
+    for (int j = 0; j < 2 * NKB; ++j) {
+      V8 pnext;
+      if (j + 1 < 2 * NKB) pnext = pstep(j + 1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int i = j * DB + db;
+        const V8 a = win[i % kWin];
+        if (i + kWin < N) win[i % kWin] = rd(i + kWin);
+        oacc[db] = Elt<BF16>::mfma(a, pcur, oacc[db]);
       }
-      const V8 a = win[i % kWin];
-      if (i + kWin < N) win[i % kWin] = rd(i + kWin);
-      oacc[i % DB] = Elt<BF16>::mfma(a, pb, oacc[i % DB]);
+      if (j + 1 < 2 * NKB) {
+        l_run = psum8<BF16>(pnext, l_run);
+        pcur = pnext;
+      }
     }
   }
 
