@@ -3,8 +3,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-A "step" is one forward pass of the op over the bench workload (BASELINE
-config 2: B=4 H=16 Hk=16 Sq=Sk=2048 d=128 bf16 with a 10% -inf additive mask),
+A "step" is one forward pass of the op over the bench workload (benchmark
+config cfg2: B=4 H=16 Hk=16 Sq=Sk=2048 d=128 bf16 with a 10% -inf additive mask),
 inputs resident in HBM. Prints ONE JSON line:
   value        = effective TFLOPS (4·B·H·Sq·Sk·d per step, the reference's
                  FLOP count, benchmark/benchmark_fa.py:135-137) over K steps
@@ -131,7 +131,7 @@ def cpu_baseline(cfg, seconds):
 
 
 def cpu_configs(seconds_each):
-    """The same CPU path on every BASELINE config: whole (b, h) heads for up to
+    """The same CPU path on every benchmark config (cfg1-cfg5): whole (b, h) heads for up to
     ``seconds_each`` each, extrapolated to the full workload (cfg1, the
     reference's CPU plumbing case, runs whole)."""
     import torch

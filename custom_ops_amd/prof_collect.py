@@ -1,6 +1,6 @@
 """Collect the rocprofv3 evidence for one configuration and write text summaries.
 
-    python -m custom_ops_amd.prof_collect --config cfg2 --out gpurun_out/profiles
+    python -m custom_ops_amd.prof_collect --config cfg2 --out prof_out
 
 Runs, each as its own rocprofv3 process under a hard time limit (this process
 never touches the GPU itself):
@@ -104,7 +104,7 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--iters", type=int, default=20)
-    ap.add_argument("--out", default=os.path.join(ROOT, "gpurun_out", "profiles"))
+    ap.add_argument("--out", default=os.path.join(ROOT, "prof_out"))
     args = ap.parse_args()
     args.out = os.path.abspath(args.out)      # the passes run with cwd=/tmp
     os.makedirs(args.out, exist_ok=True)

@@ -18,7 +18,7 @@ Three restatements of the reference's math, each pinned differently
                        online softmax (csrc/fa/common/softmax.h:65-151), P rounded
                        to the dtype (csrc/fa/sm89/fa_fwd_kernel.h:384), optional
                        split-KV + LSE combine (fa_fwd_kernel.h:1406-1545).
-* ``torch_math_cpu`` — the reference's "CPU path" as BASELINE.md defines it:
+* ``torch_math_cpu`` — the reference's CPU path as the benchmark defines it:
                        PyTorch fp32 math attention on host cores, chunked per
                        (b, h) to bound memory. Used as the timed CPU baseline.
 """

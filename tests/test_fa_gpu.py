@@ -494,7 +494,7 @@ def test_golden_fixtures(ops, gpu):
             assert np.all(out[:, :, r, :] == 0), f"{fx.name}: masked row {r} not 0"
 
 
-# ── BASELINE configurations at full size ───────────────────────────────────────
+# ── benchmark configurations cfg2-cfg5 at full size ───────────────────────────────────────
 @pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4", "cfg5"])
 def test_baseline_config(ops, gpu, name):
     from custom_ops_amd.workloads import CONFIGS, make_inputs
