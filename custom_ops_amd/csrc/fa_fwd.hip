@@ -288,7 +288,6 @@ __device__ __forceinline__ TileIdx tile_index(const KParams& p) {
 // latencies. 4 waves (BM = 128) serve small grids and split-KV. K, V and the
 // mask tile arrive by LDS DMA; V is read transposed.
 //  sK   [kBN][D]    unit c of row r at slot c ^ (r % UPR)   (π-permuted rows)
-//  sM   [BM][kBN]   unit u of row m at slot u ^ ((m/2) % 8)
 //  sV   [kBN][D]    natural key order, unit c of row r at slot c ^ swzV(r); the
 //                   PV operand Vᵀ is read with ds_read_b64_tr_b16 (in each 16-lane
 //                   group, source lane s reads 4 d-values of key base + s/4 and
@@ -299,10 +298,10 @@ template <int D, int WAVES> struct Geo {
   static constexpr int kThreads = 64 * WAVES;
   static constexpr int kUPR = D / 8;
   static constexpr int kKElems = kBN * D;
-  static constexpr int kMElems = kBM * kBN;
   static constexpr int kVElems = kBN * D;
-  static constexpr int kKWaveLoads = kBN * kUPR / 64 / kWaves;
+  static constexpr int kMElems = kBM * kBN;
   static constexpr int kMWaveLoads = kBM * 8 / 64 / kWaves;
+  static constexpr int kKWaveLoads = kBN * kUPR / 64 / kWaves;
 };
 
 template <int D> __device__ __forceinline__ int v_swz(int r) {
@@ -310,9 +309,8 @@ template <int D> __device__ __forceinline__ int v_swz(int r) {
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
 __device__ __forceinline__ int mask_swz(int m) { return (m >> 1) & 7; }
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 struct Attn {
@@ -330,14 +328,21 @@ struct Attn {
   static constexpr bool mdirect = MDIRECT;
   uint32_t k_off[G::kKWaveLoads];
   uint32_t v_off[G::kKWaveLoads];
-  uint32_t m_off[G::kMWaveLoads];
+  // Mask path. MREG (8 waves, 16-byte aligned rows): each lane loads the 32
+  // mask values of its own row straight into registers. Otherwise the tile
+  // goes through LDS (sM), loaded with 8 lanes per 128-byte row segment:
+  // those grids stream from HBM (4 waves) or read unaligned rows, where the
+  // per-row register loads (32 cache lines per instruction) cost more than
+  // the LDS round trip.
+  static constexpr bool MREG = MDIRECT && WAVES == 8;
+  uint32_t m_off[MREG ? 1 : G::kMWaveLoads];
   uint32_t k_rd[KD];
   uint32_t v_rd[DB];
   uint32_t m_rd[4];
   V8 qreg[KD];
   f32x16 oacc[DB];
   f32x16 s[NKB];
-  u32x4 mreg[MDIRECT ? 1 : G::kMWaveLoads];
+  u32x4 mreg[MREG ? 4 : (MDIRECT ? 1 : G::kMWaveLoads)];
   // Scores live in the reference's unscaled domain u = q·k + mask·(1/scale)
   // (csrc/fa/sm89/fa_fwd_kernel.h:286-310); m_run is a max of u, and
   // exp(x - max) = exp2(u·c2 - m_run·c2) with c2 = scale·log2(e) (softmax.h:87).
@@ -367,11 +372,22 @@ struct Attn {
       k_off[i] = (uint32_t)(key * p.k_rs + (slot ^ (r % G::kUPR)) * 8) * 2u;
       v_off[i] = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
     }
+    if constexpr (MREG) {
+      // lane (row l32, half g) holds keys 16g .. 16g+15 of each 32-key block
+      m_off[0] = (uint32_t)((ti.m0 + wave * 32 + l32) * p.m_rs + 16 * g) * 2u;
+    } else {
 #pragma unroll
-    for (int i = 0; i < G::kMWaveLoads; ++i) {
-      const int u = (wave * G::kMWaveLoads + i) * 64 + lane;   // the wave's own 32 rows
-      const int m = u / 8, slot = u % 8;
-      m_off[i] = (uint32_t)((ti.m0 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
+      for (int i = 0; i < G::kMWaveLoads; ++i) {
+        const int u = (wave * G::kMWaveLoads + i) * 64 + lane;   // the wave's own 32 rows
+        const int m = u / 8, slot = u % 8;
+        m_off[i] = (uint32_t)((ti.m0 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
+      }
+      const int mr = wave * 32 + l32;
+#pragma unroll
+      for (int i = 0; i < 2 * NKB; ++i) {
+        const int u = (i / 2) * 4 + 2 * g + (i % 2);
+        m_rd[i] = (uint32_t)(mr * kBN + ((u ^ mask_swz(mr)) * 8)) * 2u;
+      }
     }
     {
       // transpose-read source lane s (in its 16-lane group) reads key row
@@ -389,12 +405,6 @@ struct Attn {
     for (int kd = 0; kd < KD; ++kd) {
       const int c = 2 * kd + g;
       k_rd[kd] = (uint32_t)(l32 * G::kUPR + (c ^ (l32 % G::kUPR))) * 16u;
-    }
-    const int mr = wave * 32 + l32;
-#pragma unroll
-    for (int i = 0; i < 2 * NKB; ++i) {
-      const int u = (i / 2) * 4 + 2 * g + (i % 2);
-      m_rd[i] = (uint32_t)(mr * kBN + ((u ^ mask_swz(mr)) * 8)) * 2u;
     }
 #pragma unroll
     for (int i = 0; i < DB; ++i) oacc[i] = f32x16{};
@@ -420,38 +430,48 @@ struct Attn {
       bload16_lds(r, lds_addr(sK) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), k_off[i]);
   }
 
-  // Mask tile n: LDS DMA when rows are 16-byte aligned, else registers
-  // (commit_m writes them); chunks reaching past Sk are read element by element.
+  // Mask tile n. MREG: straight into registers, chunk i (8 keys, 16 bytes)
+  // holding keys 32(i/2) + 16g + 8(i%2) of the tile (a chunk that starts
+  // below Sk ends inside its row: the row stride is a multiple of 8 >= Sk).
+  // Otherwise into the wave's own rows of sM: by LDS DMA when rows are
+  // 16-byte aligned, else through registers (commit_m stores them), reading
+  // chunks that reach past Sk element by element.
+  static __device__ __forceinline__ constexpr uint32_t chunk_off(int i) {
+    return (uint32_t)(32 * (i / 2) + 8 * (i % 2)) * 2u;
+  }
   __device__ __forceinline__ void issue_m(int n, uint16_t* sM) {
     const uint32_t key0 = (uint32_t)n * kBN;
-    if constexpr (MDIRECT) {
+    if constexpr (MREG) {
+      const rsrc_t r = make_rsrc(reinterpret_cast<const char*>(mbase) + key0 * 2u, mbytes - key0 * 2u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mreg[i] = bload16(r, m_off[0] + chunk_off(i));
+    } else if constexpr (MDIRECT) {
       const i32x4 r = make_rsrc_words(reinterpret_cast<const char*>(mbase) + key0 * 2u, mbytes - key0 * 2u);
 #pragma unroll
       for (int i = 0; i < G::kMWaveLoads; ++i)
         bload16_lds(r, lds_addr(sM) + (uint32_t)((wave * G::kMWaveLoads + i) * 64 * 16), m_off[i]);
-      return;
     } else {
 #pragma unroll
-    for (int i = 0; i < G::kMWaveLoads; ++i) {
-      const int u = (wave * G::kMWaveLoads + i) * 64 + lane;
-      const int c = (u % 8) ^ mask_swz(u / 8);
-      const int kc = (int)key0 + c * 8;
-      const uint32_t off = m_off[i] + key0 * 2u;
-      if (kc + 8 <= p.sk) {
-        mreg[i] = bload16(rm, off);
-      } else {
-        uint32_t w[4];
+      for (int i = 0; i < G::kMWaveLoads; ++i) {
+        const int u = (wave * G::kMWaveLoads + i) * 64 + lane;
+        const int c = (u % 8) ^ mask_swz(u / 8);
+        const int kc = (int)key0 + c * 8;
+        const uint32_t off = m_off[i] + key0 * 2u;
+        if (kc + 8 <= p.sk) {
+          mreg[i] = bload16(rm, off);
+        } else {
+          uint32_t w[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t lo = (kc + 2 * j < p.sk)
-              ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j, 0, 0) : 0u;
-          const uint32_t hi = (kc + 2 * j + 1 < p.sk)
-              ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j + 2, 0, 0) : 0u;
-          w[j] = (lo & 0xffffu) | (hi << 16);
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = (kc + 2 * j < p.sk)
+                ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j, 0, 0) : 0u;
+            const uint32_t hi = (kc + 2 * j + 1 < p.sk)
+                ? __builtin_amdgcn_raw_buffer_load_b16(rm, off + 4 * j + 2, 0, 0) : 0u;
+            w[j] = (lo & 0xffffu) | (hi << 16);
+          }
+          mreg[i] = u32x4{w[0], w[1], w[2], w[3]};
         }
-        mreg[i] = u32x4{w[0], w[1], w[2], w[3]};
       }
-    }
     }
   }
 
@@ -484,8 +504,14 @@ struct Attn {
     const uint8_t* mb = reinterpret_cast<const uint8_t*>(sM);
 #pragma unroll
     for (int b = 0; b < NKB; ++b) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * b]);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * b + 1]);
+      u32x4 lo, hi;
+      if constexpr (MREG) {
+        lo = mreg[2 * b];
+        hi = mreg[2 * b + 1];
+      } else {
+        lo = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * b]);
+        hi = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * b + 1]);
+      }
       const f32x16 mk = mask_to_f32<BF16>(lo, hi);
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[b][i] = mk[i] * inv_scale;
@@ -698,7 +724,7 @@ void fa_fwd_kernel(const KParams p) {
   static_assert(NST >= 2 && NST <= 4, "two to four stages");
   __shared__ __align__(16) uint16_t sK[NST][G::kKElems];
   __shared__ __align__(16) uint16_t sV[NST][G::kVElems];
-  __shared__ __align__(16) uint16_t sM[G::kMElems];
+  __shared__ __align__(16) uint16_t sM[A::MREG ? 8 : G::kMElems];
 
   const TileIdx ti = tile_index<G::kBM>(p);
   A a(p);
@@ -740,8 +766,14 @@ void fa_fwd_kernel(const KParams p) {
     constexpr int SF = (ST + NST - 1) % NST;   // stage of tile n + NST - 1 (= n - 1)
     const bool more = n + 1 < ne, far = n + NST - 1 < ne;
     if constexpr (NST == 2) wait_vmcnt<0>();
+    // A register mask can leave before the barrier (its registers were freed
+    // by the previous mask_init); the last tile reloads its own mask (unused)
+    // so the loop body has no branch there. An LDS mask waits for the barrier.
+    if constexpr (A::MREG) a.issue_m(more ? n + 1 : n, sM);
     wg_barrier();
-    if (more) a.issue_m(n + 1, sM);
+    if constexpr (!A::MREG) {
+      if (more) a.issue_m(n + 1, sM);
+    }
     // 4 waves (small grids, HBM streams): K(n+NST-1) goes out before QK(n),
     // for the longest lead. 8 waves (MFMA-bound): after it, so QK's K-operand
     // reads do not share the LDS with the incoming K tile (cfg2 -1.4 %,
@@ -756,7 +788,14 @@ void fa_fwd_kernel(const KParams p) {
     if (far) a.issue_v(n + NST - 1, sV[SF]);
     a.apply_tail(n);
     a.softmax_pv(sV[ST]);
-    if (more) {
+    if constexpr (A::MREG) {
+      // widen mask(n + 1) into the accumulators (the compiler waits for its
+      // loads, and with them for the K/V DMAs issued later). Kept inside this
+      // iteration: hoisted past the next barrier it would hold mask(n + 1)'s
+      // registers across mask(n + 2)'s loads.
+      a.mask_init(sM);
+      __builtin_amdgcn_sched_barrier(0);
+    } else if (more) {
       if (far) wait_vmcnt<kKVLoads>();
       else wait_vmcnt<0>();
       a.commit_m(sM);
