@@ -1,23 +1,30 @@
 #!/usr/bin/env python3
 """Benchmark of recsys_ops::mha_fwd_with_mask on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
 
 A "step" is one forward pass of the op over the bench workload (benchmark
-config cfg2: B=4 H=16 Hk=16 Sq=Sk=2048 d=128 bf16 with a 10% -inf additive mask),
-inputs resident in HBM. Prints ONE JSON line:
+config cfg2: B=4 H=16 Hk=16 Sq=Sk=2048 d=128 bf16 with a 10% -inf additive
+mask), inputs resident in HBM. Each timed step starts from cold, clean caches:
+a 512 MB buffer is zeroed AND read back before it (so neither L2 nor the MALL
+holds the inputs or dirty flush lines), then the call is bracketed by HIP
+events on the op's stream. Prints ONE JSON line:
   value        = effective TFLOPS (4·B·H·Sq·Sk·d per step, the reference's
-                 FLOP count, benchmark/benchmark_fa.py:135-137) over K steps
+                 FLOP count, benchmark/benchmark_fa.py:135-137) at the MEDIAN
+                 event time of the K cold steps (the benchmark's definition:
+                 hipEvent median of >= 50 iterations after a >= 512 MB flush)
+  us_hot       = back-to-back launches at settled clocks (no flush), extra key
   roofline     = dominant kernel (fa_fwd_kernel) achieved TFLOP/s vs the
-                 MI355X dense bf16 MFMA peak, from HIP events on the launch stream
-  configs      = per-config latency (µs): "us" the reference's way (median of
-                 N after warmup, a 256 MB buffer zeroed before each iteration,
-                 benchmark/benchmark_fa.py:115-132); "us_cold" with a 512 MB
-                 buffer zeroed AND read back (cold, clean L2 + MALL: no dirty
-                 flush lines to write back inside the timed call); "us_hot"
-                 back-to-back launches at settled clocks
+                 MI355X dense bf16 MFMA peak, from the mean of the same cold
+                 event times; traffic and the mask stream from the committed
+                 rocprofv3 counter summaries (profiles/)
+  configs      = per-config latency (µs): "us_cold" (as value), "us" the
+                 reference's way (a 256 MB buffer zeroed before each iteration,
+                 median, benchmark/benchmark_fa.py:115-132), "us_hot"
   cpu_baseline = PyTorch fp32 math attention on this host's cores over a
-                 time-bounded sample of (b, h) heads of the same workload.
+                 bounded sample of whole (b, h) heads of every config; each
+                 config timed 3 times in the same order and thread count, the
+                 median reported with its spread; value = the cfg2 row.
 """
 import argparse
 import json
@@ -36,13 +43,14 @@ MI355X_HBM_GBPS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--settle-s", type=float, default=0.5,
                     help="untimed back-to-back steps before warmup, in seconds (clock ramp)")
     ap.add_argument("--ref-iters", type=int, default=50)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="CPU work per config per repetition (3 repetitions)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     return ap.parse_args()
@@ -88,83 +96,79 @@ def hot_us(fn, iters=100):
     return e0.elapsed_time(e1) / iters * 1e3
 
 
-def cpu_baseline(cfg, seconds):
-    """PyTorch fp32 math path (the reference's CPU path) on host cores."""
+def _cpu_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or ""
+
+
+def cpu_baseline(seconds: float, reps: int = 3):
+    """PyTorch fp32 math attention (the reference's CPU path) on host cores.
+
+    For every config, in a fixed order: whole (b, h) heads are timed ``reps``
+    times; the head count per repetition is fixed by a probe so that one
+    repetition takes about ``seconds`` (all heads if they fit). Each
+    repetition is extrapolated to the whole workload; the median and the
+    spread (min, max) over repetitions are reported."""
     import torch
-    from custom_ops_amd.workloads import make_inputs
-    from oracle.oracle import torch_math_cpu
+    from custom_ops_amd.workloads import CONFIGS, make_inputs
+    from oracle.oracle import oracle_fwd, torch_math_cpu
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores) or cores))
     torch.set_num_threads(cores)
-    q, k, v, m = make_inputs(cfg)
-    heads = [(b, h) for b in range(cfg.B) for h in range(cfg.H)]
-    torch_math_cpu(q, k, v, m, heads=heads[:1])   # warm-up
-    done = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:   # whole (b, h) heads, cycling over the batch
-        torch_math_cpu(q, k, v, m, heads=[heads[done % len(heads)]])
-        done += 1
-    el = time.perf_counter() - t0
-    flops = cfg.flops / len(heads) * done
-    cpu_name = platform.processor() or ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_name = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {
-        "value": round(flops / el / 1e12, 5),
-        "unit": "TFLOPS",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"{done} (b,h) head passes ({done / len(heads):.1f}x the {len(heads)} heads of "
-                  f"{cfg.name}) in {el:.1f}s, fp32 torch math "
-                  f"attention (scores+mask, guarded softmax, P@V) on {cpu_name}",
-        "us_full_workload_extrapolated": round(el / done * len(heads) * 1e6, 1),
-    }
-
-
-def cpu_configs(seconds_each):
-    """The same CPU path on every benchmark config (cfg1-cfg5): whole (b, h) heads for up to
-    ``seconds_each`` each, extrapolated to the full workload (cfg1, the
-    reference's CPU plumbing case, runs whole)."""
-    import torch
-    from custom_ops_amd.workloads import CONFIGS, make_inputs
-    from oracle.oracle import torch_math_cpu
     out = {}
-    for name in ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5"):
+    for name in ("cfg2", "cfg3", "cfg4", "cfg5", "cfg1"):
         c = CONFIGS[name]
         q, k, v, m = make_inputs(c)
         heads = [(b, h) for b in range(c.B) for h in range(c.H)]
-        torch_math_cpu(q, k, v, m, heads=heads[:1])
-        done = 0
+        torch_math_cpu(q, k, v, m, heads=heads[:2])           # warm-up
         t0 = time.perf_counter()
-        while done < len(heads) and (done == 0 or time.perf_counter() - t0 < seconds_each):
-            torch_math_cpu(q, k, v, m, heads=[heads[done]])
-            done += 1
-        el = time.perf_counter() - t0
-        us_full = el / done * len(heads) * 1e6
-        out[name] = {"us": round(us_full, 1),
-                     "tflops": round(c.flops / (us_full * 1e-6) / 1e12, 5),
-                     "heads_timed": f"{done}/{len(heads)}",
-                     "extrapolated": done < len(heads)}
+        torch_math_cpu(q, k, v, m, heads=heads[:2])           # probe
+        per = max((time.perf_counter() - t0) / 2, 1e-6)
+        n = max(1, min(len(heads), int(seconds / per)))
+        runs = []
+        for r in range(reps):
+            sel = [heads[(r * n + i) % len(heads)] for i in range(n)]
+            t0 = time.perf_counter()
+            torch_math_cpu(q, k, v, m, heads=sel)
+            runs.append((time.perf_counter() - t0) / n * len(heads) * 1e6)
+        runs.sort()
+        med = runs[len(runs) // 2]
+        out[name] = {"us": round(med, 1),
+                     "tflops": round(c.flops / (med * 1e-6) / 1e12, 5),
+                     "us_min": round(runs[0], 1), "us_max": round(runs[-1], 1),
+                     "spread_pct": round(100 * (runs[-1] - runs[0]) / med, 1),
+                     "heads_per_rep": f"{n}/{len(heads)}", "reps": reps,
+                     "extrapolated": n < len(heads)}
     # cfg1 also through the build's C restatement (one thread, fp32, the
     # reference kernel's tile-wise online softmax), whole.
-    from oracle.oracle import oracle_fwd
     c = CONFIGS["cfg1"]
     q, k, v, m = (t.float().numpy() for t in make_inputs(c))
     t0 = time.perf_counter()
     oracle_fwd(q, k, v, m, dtype="fp32", block_n=64)
-    el = time.perf_counter() - t0
-    out["cfg1"]["c_restatement_us"] = round(el * 1e6, 1)
+    out["cfg1"]["c_restatement_us"] = round((time.perf_counter() - t0) * 1e6, 1)
     out["cfg1"]["c_restatement_threads"] = 1
-    return out
+    base = out["cfg2"]
+    return {
+        "value": base["tflops"],
+        "unit": "TFLOPS",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"cfg2: {base['heads_per_rep']} whole (b,h) heads per repetition, median of "
+                  f"{reps} repetitions (spread {base['spread_pct']}%), fp32 torch math attention "
+                  f"(scores+mask, guarded softmax, P@V) on {_cpu_name()}, extrapolated to the "
+                  f"64 heads",
+        "us_full_workload": base["us"],
+        "configs": out,
+    }
 
 
 def main():
@@ -197,27 +201,40 @@ def main():
     for _ in range(args.warmup):
         fn()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        fn()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1e3 / args.steps
-    kern_ms = ev0.elapsed_time(ev1) / args.steps   # device time per launch on the op's stream
-    ms_per_step = max(wall_ms, kern_ms)
-    value = cfg.flops / (ms_per_step * 1e-3) / 1e12
-    achieved = cfg.flops / (kern_ms * 1e-3) / 1e12
 
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", "traffic_fa_fwd_kernel_cfg2.json")
-    if os.path.exists(tfile):
-        with open(tfile) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    # Timed region: K steps, each from cold clean caches (512 MB zeroed and read
+    # back, not timed), the call bracketed by events on the op's stream.
+    stream = torch.cuda.current_stream(dev)
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+    reread = torch.empty((), dtype=torch.int32, device=dev)
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        flush.zero_()
+        torch.amax(flush, dim=0, out=reread)
+        st[i].record(stream)
+        fn()
+        en[i].record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    ts = sorted(a.elapsed_time(b) for a, b in zip(st, en))   # ms
+    del flush
+    med_ms = ts[len(ts) // 2]
+    mean_ms = sum(ts) / len(ts)
+    value = cfg.flops / (med_ms * 1e-3) / 1e12
+    achieved = cfg.flops / (mean_ms * 1e-3) / 1e12
+    us_hot = hot_us(fn)
+
+    def profile(name):
+        path = os.path.join(ROOT, "profiles", name)
+        if os.path.exists(path):
+            with open(path) as f:
+                return json.load(f)
+        return {}
+    traffic = profile(f"traffic_fa_fwd_kernel_{cfg.name}.json")
+    mask_stream = profile(f"mask_stream_fa_fwd_kernel_{cfg.name}.json")
 
     result = {
         "metric": "masked attn fwd µs & TFLOPS (% MI355X bf16 MFMA peak), 1 GPU",
@@ -227,8 +244,15 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "clock_settle_steps": settle_n,
-        "ms_per_step": round(ms_per_step, 5),
-        "us_per_step": round(ms_per_step * 1e3, 2),
+        "ms_per_step": round(med_ms, 5),
+        "us_per_step": round(med_ms * 1e3, 2),
+        "timing": "median of the K steps' event times, each step after a 512 MB zero + "
+                  "read-back flush (cold, clean caches)",
+        "timed_region_wall_s": round(wall_s, 3),
+        "us_per_step_mean": round(mean_ms * 1e3, 2),
+        "us_per_step_min_max": [round(ts[0] * 1e3, 2), round(ts[-1] * 1e3, 2)],
+        "us_hot": round(us_hot, 2),
+        "tflops_hot": round(cfg.flops / (us_hot * 1e-6) / 1e12, 2),
         "pct_of_bf16_peak": round(100 * value / MI355X_BF16_DENSE_TFLOPS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -242,9 +266,14 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "fa_fwd_kernel<128,bf16>",
                      "achieved": round(achieved, 2), "peak": MI355X_BF16_DENSE_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MI355X_BF16_DENSE_TFLOPS, 4),
-                     "traffic": traffic, "avg_launch_us": round(kern_ms * 1e3, 2),
+                     "traffic": traffic.get("hbm_bytes_per_launch"),
+                     "avg_launch_us": round(mean_ms * 1e3, 2),
+                     "avg_launch_timing": "mean of the cold steps' event times",
                      "algorithmic_flop_per_launch": cfg.flops,
-                     "algorithmic_bytes_per_launch": cfg.algorithmic_bytes},
+                     "algorithmic_bytes_per_launch": cfg.algorithmic_bytes,
+                     "mask_stream": {k: mask_stream.get(k) for k in (
+                         "mask_bytes_algorithmic", "mask_hbm_bytes_counted",
+                         "mask_hbm_gbps_counted", "source")} if mask_stream else None},
     }
 
     if not args.no_configs:
@@ -261,9 +290,9 @@ def main():
             fnc = lambda: ops.mha_fwd_with_mask(tq, tk, tv, tm)  # noqa: E731
             us = ref_method_us(fnc, 10, args.ref_iters, flush_ref)
             us_cold = ref_method_us(fnc, 5, args.ref_iters, flush_big, reread)
-            us_hot = hot_us(fnc)
+            us_hot_c = hot_us(fnc)
             confs[name] = {"us": round(us, 2)}
-            for key, t in (("", us), ("_cold", us_cold), ("_hot", us_hot)):
+            for key, t in (("", us), ("_cold", us_cold), ("_hot", us_hot_c)):
                 tf = c.flops / (t * 1e-6) / 1e12
                 confs[name]["us" + key] = round(t, 2)
                 confs[name]["tflops" + key] = round(tf, 2)
@@ -275,8 +304,7 @@ def main():
         result["configs"] = confs
 
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
-        result["cpu_baseline"]["configs"] = cpu_configs(2.0)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
 
     print(json.dumps(result), flush=True)
 

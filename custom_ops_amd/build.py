@@ -2,13 +2,18 @@
 
 hipcc cross-compiles without a GPU, so this runs on any host with ROCm.
 Usage: ``python -m custom_ops_amd.build`` (or ``__graft_entry__.build()``).
+Every build also checks the gfx950 assembly it produced
+(``custom_ops_amd.isa_check``) and refuses to install a library that
+violates those properties.
 """
 from __future__ import annotations
 
+import glob
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -42,17 +47,39 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (expected /opt/rocm/bin/hipcc)")
 
 
+def compile_checked(out_path: str, flags=None, verbose: bool = False) -> str:
+    """Compile SRC into ``out_path`` (atomically) after checking the device
+    assembly of that same compilation; raise RuntimeError on either failure."""
+    from .isa_check import violations
+    flags = list(HIPCC_FLAGS if flags is None else flags)
+    with tempfile.TemporaryDirectory(prefix="mi355fa-build-") as tmp:
+        product = os.path.join(tmp, os.path.basename(out_path))
+        cmd = [hipcc(), *flags, f"-I{INCLUDE}", SRC, "-o", product, "-save-temps=obj"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True, cwd=tmp)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+        asm = sorted(glob.glob(os.path.join(tmp, "*amdgcn-amd-amdhsa*.s")))
+        if not asm:
+            raise RuntimeError("hipcc left no device assembly to check")
+        bad = []
+        for path in asm:
+            with open(path) as f:
+                bad += [f"{os.path.basename(path)}: {v}" for v in violations(f.read())]
+        if bad:
+            raise RuntimeError("device assembly check failed; library not installed:\n"
+                               + "\n".join(bad))
+        tmp_out = out_path + ".tmp"
+        shutil.copyfile(product, tmp_out)
+        os.chmod(tmp_out, 0o755)
+        os.replace(tmp_out, out_path)
+    return out_path
+
+
 def build(verbose: bool = False) -> str:
     """Compile the library (always recompiles) and return its path."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", SRC, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    return compile_checked(LIB_PATH, verbose=verbose)
 
 
 if __name__ == "__main__":

@@ -176,9 +176,7 @@ def register() -> None:
 def num_splits_for(q, k, v, mask) -> int:
     """The split count the library would use for these inputs (host query)."""
     validate(q, k, v, mask)
-    out = torch.empty((0,), dtype=q.dtype, device=q.device)
-    p = make_params(q, k, v, mask, out)
-    p.o = q.data_ptr()
+    p = make_params(q, k, v, mask, q)   # planning reads shapes only; q stands in for out
     with torch.cuda.device(q.device):
         return _lib.num_splits(p)
 

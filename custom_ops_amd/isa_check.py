@@ -1,0 +1,63 @@
+"""Checks on the gfx950 assembly of this library's own kernels, run by every
+build (``custom_ops_amd.build.build``) so that a library violating them is
+never produced, and by ``tests/test_isa.py``.
+
+* M0 is written only inside the inline-assembly LDS DMA. The asm names M0 as
+  a clobber; the compiler reserves M0 and does not track that clobber, so it
+  must keep no value of its own in M0 anywhere in these kernels (it uses M0
+  only for LDS DMA, LDS-parameter and s_sendmsg-style operations, none of
+  which the kernels use outside the asm).
+* No packed-FP32 arithmetic (``v_pk_{add,mul,fma}_f32``): the build disables
+  the feature; this catches a flag that went missing.
+* No register spills and no scratch memory in any kernel (a kernel that fell
+  back to scratch ran 16x slower while still passing every numeric test).
+"""
+from __future__ import annotations
+
+import re
+
+
+def code_outside_asm(text: str):
+    """Instruction lines of the assembly that are not inside an inline-asm block."""
+    inside = False
+    for line in text.splitlines():
+        if ";;#ASMSTART" in line:
+            inside = True
+            continue
+        if ";;#ASMEND" in line:
+            inside = False
+            continue
+        code = line.split(";", 1)[0].strip()
+        if not inside and code:
+            yield code
+
+
+def kernel_metadata(text: str):
+    """(name, {field: value}) for every kernel in the code-object metadata."""
+    meta = text[text.index("amdhsa.kernels:"):]
+    for block in meta.split("\n  - ")[1:]:
+        name = re.search(r"\.name:\s+(\S+)", block)
+        if not name:
+            continue
+        fields = dict(re.findall(r"\.(\w+):\s+(\d+)\s*$", block, re.M))
+        yield name.group(1), fields
+
+
+def violations(text: str) -> list:
+    """Human-readable list of every violated property (empty when clean)."""
+    out = []
+    if ";;#ASMSTART" not in text:
+        out.append("the LDS DMA inline assembly is missing")
+    m0 = [c for c in code_outside_asm(text) if re.search(r"\bm0\b", c)]
+    if m0:
+        out.append(f"M0 used outside the LDS DMA asm: {m0[:5]}")
+    pk = [c for c in code_outside_asm(text) if re.match(r"v_pk_(add|mul|fma)_f32\b", c)]
+    if pk:
+        out.append(f"packed FP32 arithmetic: {pk[:5]}")
+    for name, f in kernel_metadata(text):
+        if (int(f.get("vgpr_spill_count", 0)) or int(f.get("sgpr_spill_count", 0))
+                or int(f.get("private_segment_fixed_size", 0))):
+            out.append(f"spills or scratch in {name}: {f}")
+    if "scratch_" in "\n".join(code_outside_asm(text)):
+        out.append("scratch instructions present")
+    return out

@@ -1,31 +1,36 @@
-"""Deployment loading for the ``fa`` op group: offline build with a metadata
-sidecar, validated precompiled load, fail-closed dispatcher ownership.
+"""Deployment loading for the ``fa`` op group.
 
-Mirrors the reference's ``CustomOps.build`` / ``load_precompiled`` / ``load``
-contract (__init__.py:654-1011) for this build's artifact, a C-ABI HIP library
-opened with ctypes (the torch op is registered from Python over it):
+Contract kept from the reference facade (``CustomOps.build`` /
+``load_precompiled`` / ``load``, __init__.py:654-1011, and ``FAOps``,
+recsys.py:165-202): an offline build that publishes the library together with
+a metadata sidecar; a precompiled load that validates everything it can
+BEFORE the library is opened and then verifies the registered operator
+(schema, Meta kernel); a strict mode in which nothing is compiled; and one
+owner per dispatcher operator per process (a second library for the same
+operator, a modified file, or an operator registered behind the loader's
+back fails closed).
 
-* ``FAOps().build(out_dir)`` compiles ``libmi355_fa.so`` for gfx950 into
-  ``out_dir`` and publishes ``libmi355_fa.so.json`` next to it (schema contract,
-  offload targets, runtime compatibility, source/toolchain fingerprints,
-  library SHA-256 and size). It never loads what it builds and refuses to
-  overwrite a library already loaded in this process.
-* ``FAOps().load_precompiled(path)`` validates the sidecar against this Python
-  wrapper and the running process BEFORE opening the library (missing,
-  tampered or incompatible artifacts raise ``CustomOpsError``; nothing falls
-  back to compiling), then opens it, checks the ABI and exported symbols,
-  registers ``recsys_ops::mha_fwd_with_mask`` and verifies its schema and Meta
-  kernel before reporting the group available.
-* ``load()`` is the development path: the in-tree library, compiled by hipcc
-  when missing and ``allow_jit`` is True. With ``allow_jit=False`` it only
-  accepts a group already loaded by ``load_precompiled``.
+This module's own design for that contract:
 
-One library per process owns the operator: loading a different file (another
-build, or a copy of the same bytes) for the same operator, or an operator that
-another library already registered, raises instead of replacing it.
+* The sidecar is a *sealed artifact manifest* (``ARTIFACT_FORMAT``) with four
+  sections — ``contract`` (operator namespace, schemas, Meta ops, C ABI),
+  ``runtime`` (torch major.minor, HIP major), ``targets`` (gfx names) and
+  ``provenance`` (sources digest, flags, compiler) — plus ``payload`` (file
+  name, size, SHA-256). ``seal`` is the SHA-256 of the canonical JSON of all
+  of them, so any edit of the sidecar is caught before its content is
+  trusted.
+* Validation is a table of named checks (``_CHECKS``), each comparing one
+  section with what this process expects and returning a message, so the
+  error says which section disagreed and how.
+* Ownership is an explicit state machine per operator in ``_REGISTRY``:
+  a claim is ``reserved`` before the library is opened, ``live`` once its
+  operator verified, ``broken`` if anything failed in between (the process
+  must be restarted to retry, as a half-registered operator cannot be
+  removed from the dispatcher).
 """
 from __future__ import annotations
 
+import dataclasses
 import fcntl
 import hashlib
 import json
@@ -35,123 +40,221 @@ import subprocess
 import tempfile
 import threading
 from pathlib import Path
-from typing import Optional
+from typing import Callable, Optional
 
 import torch
 
 from . import _lib, build as _build, fa
 
-METADATA_VERSION = 1
-PRODUCER = "custom_ops_amd"
-
-_LOCK = threading.RLock()
-_LIBRARIES: dict = {}    # identity -> record
-_OP_OWNERS: dict = {}    # "ns::op" -> identity
+ARTIFACT_FORMAT = "custom_ops_amd.artifact/2"
+GROUP_VERSION = "1"
 
 
 class CustomOpsError(RuntimeError):
     """Load/build failure (the reference's exception type name, __init__.py:71)."""
 
 
-def _json_hash(value) -> str:
-    return hashlib.sha256(json.dumps(value, sort_keys=True).encode()).hexdigest()
+# ── artifact manifest ─────────────────────────────────────────────────────────
+
+def _canonical(obj) -> bytes:
+    return json.dumps(obj, sort_keys=True, separators=(",", ":")).encode()
 
 
-def _metadata_fingerprint(metadata: dict) -> str:
-    return _json_hash({k: v for k, v in metadata.items()
-                       if k not in ("build_fingerprint", "library")})
+def seal_of(manifest: dict) -> str:
+    """SHA-256 over every section except the seal itself."""
+    return hashlib.sha256(_canonical({k: v for k, v in manifest.items() if k != "seal"})).hexdigest()
 
 
-def _file_sha256(path: Path) -> str:
+def _digest_file(path: Path) -> str:
     h = hashlib.sha256()
     with path.open("rb") as f:
-        for chunk in iter(lambda: f.read(1 << 20), b""):
-            h.update(chunk)
-    return h.hexdigest()
+        while True:
+            block = f.read(1 << 20)
+            if not block:
+                return h.hexdigest()
+            h.update(block)
 
 
-def _file_stat(path: Path) -> tuple:
-    st = path.stat()
-    return (st.st_dev, st.st_ino, st.st_size, st.st_mtime_ns)
+def _runtime_section() -> dict:
+    """What a library built by this process's toolchain needs from a loading process."""
+    hip = (getattr(torch.version, "hip", None) or "").split(".")[0]
+    return {"torch": ".".join(torch.__version__.split("+")[0].split(".")[:2]), "hip": hip}
 
 
-def _library_identity(path: Path) -> tuple:
-    """(device, inode, sha256): the same file with the same bytes."""
-    st = _file_stat(path)
-    return (st[0], st[1], _file_sha256(path)), st
+_GFX = re.compile(r"gfx[0-9a-f]{3,4}")
 
 
-def _runtime_compatibility() -> dict:
-    """What a library built here needs from the process that loads it."""
-    hip = getattr(torch.version, "hip", None) or ""
-    return {
-        "abi_version": _lib.ABI_VERSION,
-        "torch": ".".join(torch.__version__.split("+")[0].split(".")[:2]),
-        "hip_major": hip.split(".")[0] if hip else "",
-    }
-
-
-def _canonical_archs(value) -> list:
-    """Sorted unique gfx targets; rejects anything that is not 'gfx' + digits/letters."""
-    items = value.split(";") if isinstance(value, str) else list(value)
-    out = sorted({s.strip() for s in items if str(s).strip()})
-    for a in out:
-        if not re.fullmatch(r"gfx[0-9a-f]{3,4}", a):
-            raise CustomOpsError(f"invalid offload target {a!r} (expected e.g. 'gfx950')")
+def _targets(value) -> list:
+    """Sorted unique gfx names from 'gfx950;gfx942' or a list; rejects malformed names."""
+    names = value.split(";") if isinstance(value, str) else list(value)
+    out = sorted({str(n).strip() for n in names if str(n).strip()})
+    bad = [n for n in out if not _GFX.fullmatch(n)]
+    if bad:
+        raise CustomOpsError(f"invalid offload target(s) {bad} (expected names like 'gfx950')")
     return out
 
 
 def _visible_archs() -> set:
-    """gfx names of the visible GPUs (empty without a GPU)."""
+    """gfx names of the GPUs this process can see (empty without a GPU)."""
     if not torch.cuda.is_available():
         return set()
     return {torch.cuda.get_device_properties(i).gcnArchName.split(":")[0]
             for i in range(torch.cuda.device_count())}
 
 
-def _has_schema(qualified: str) -> bool:
+def _registered_schema(qualified: str) -> Optional[str]:
     try:
-        return bool(torch._C._jit_get_schemas_for_operator(qualified))
+        found = torch._C._jit_get_schemas_for_operator(qualified)
     except RuntimeError:
-        return False
+        return None
+    return str(found[0]) if found else None
 
 
-def _schema(qualified: str) -> str:
-    schemas = torch._C._jit_get_schemas_for_operator(qualified)
-    return str(schemas[0]) if schemas else ""
+@dataclasses.dataclass(frozen=True)
+class _Expectation:
+    """What the loading process requires of an artifact."""
+    contract: dict
+    runtime: dict
+    visible: frozenset
 
 
-def _hipcc_version(hipcc: str) -> str:
-    try:
-        out = subprocess.run([hipcc, "--version"], capture_output=True, text=True, timeout=60)
-        for line in out.stdout.splitlines():
-            if "version" in line.lower():
-                return line.strip()
-    except (OSError, subprocess.SubprocessError):
-        pass
-    return ""
+def _section_diff(name: str, got, want) -> Optional[str]:
+    if got == want:
+        return None
+    if isinstance(got, dict) and isinstance(want, dict):
+        keys = sorted(set(got) | set(want))
+        diff = [f"{k}: artifact={got.get(k)!r} process={want.get(k)!r}"
+                for k in keys if got.get(k) != want.get(k)]
+        return f"{name} mismatch ({'; '.join(diff)})"
+    return f"{name} mismatch: artifact={got!r} process={want!r}"
 
+
+def _check_format(md: dict, exp: _Expectation, lib: Path) -> Optional[str]:
+    if md.get("format") != ARTIFACT_FORMAT:
+        return f"format mismatch: artifact={md.get('format')!r} process={ARTIFACT_FORMAT!r}"
+    missing = [k for k in ("contract", "runtime", "targets", "provenance", "payload", "seal")
+               if k not in md]
+    return f"sidecar lacks section(s) {missing}" if missing else None
+
+
+def _check_seal(md: dict, exp: _Expectation, lib: Path) -> Optional[str]:
+    if not isinstance(md["seal"], str) or md["seal"] != seal_of(md):
+        return "sidecar seal is broken (the metadata was edited after the build)"
+    return None
+
+
+def _check_contract(md: dict, exp: _Expectation, lib: Path) -> Optional[str]:
+    return _section_diff("contract", md["contract"], exp.contract)
+
+
+def _check_runtime(md: dict, exp: _Expectation, lib: Path) -> Optional[str]:
+    return _section_diff("runtime", md["runtime"], exp.runtime)
+
+
+def _check_targets(md: dict, exp: _Expectation, lib: Path) -> Optional[str]:
+    t = md["targets"]
+    if not isinstance(t, list) or not t or t != _targets(t):
+        return "targets must be a non-empty sorted list of gfx names"
+    uncovered = sorted(exp.visible - set(t))
+    if uncovered:
+        return f"target mismatch: the visible GPU(s) {uncovered} are not among the built {t}"
+    return None
+
+
+def _check_payload(md: dict, exp: _Expectation, lib: Path) -> Optional[str]:
+    pl = md["payload"]
+    if not isinstance(pl, dict) or pl.get("file") != lib.name:
+        return f"payload names {pl.get('file') if isinstance(pl, dict) else pl!r}, not {lib.name!r}"
+    size = lib.stat().st_size
+    if type(pl.get("bytes")) is not int or pl["bytes"] != size:
+        return f"payload size mismatch: sidecar {pl.get('bytes')!r} bytes, file {size}"
+    if pl.get("sha256") != _digest_file(lib):
+        return "payload digest mismatch: the library file differs from the one built"
+    return None
+
+
+_CHECKS: tuple = (
+    ("format", _check_format),
+    ("seal", _check_seal),
+    ("contract", _check_contract),
+    ("runtime", _check_runtime),
+    ("targets", _check_targets),
+    ("payload", _check_payload),
+)
+
+
+# ── operator ownership ────────────────────────────────────────────────────────
+
+@dataclasses.dataclass
+class _Claim:
+    path: Path
+    identity: tuple          # (st_dev, st_ino, sha256)
+    state: str = "reserved"  # reserved -> live | broken
+    reason: str = ""
+
+
+_REGISTRY: dict = {}         # qualified op name -> _Claim
+_LOCK = threading.RLock()
+
+
+def _identity(path: Path) -> tuple:
+    st = path.stat()
+    return (st.st_dev, st.st_ino, _digest_file(path))
+
+
+def _claim(ops: list, path: Path, identity: tuple) -> list:
+    """Reserve ``ops`` for the library at ``path`` or raise; returns the claims
+    (existing live ones are reused: loading the same file twice is idempotent)."""
+    claims = []
+    for op in ops:
+        c = _REGISTRY.get(op)
+        if c is None:
+            if _registered_schema(op) is not None:
+                raise CustomOpsError(
+                    f"{op} is registered outside this loader (untracked library); "
+                    "start a fresh process")
+            continue
+        if c.identity[:2] == identity[:2] and c.identity[2] != identity[2]:
+            raise CustomOpsError(f"{c.path} changed on disk after it was loaded; "
+                                 "start a fresh process")
+        if c.identity != identity:
+            raise CustomOpsError(f"{op} is already served by {c.path}; a second library "
+                                 "(another build or a copy) cannot serve it in this process")
+        if c.state == "broken":
+            raise CustomOpsError(f"an earlier load of {c.path} failed midway ({c.reason}); "
+                                 "start a fresh process")
+        claims.append(c)
+    if len(claims) == len(ops):
+        return claims
+    new = _Claim(path=path, identity=identity)
+    for op in ops:
+        _REGISTRY.setdefault(op, new)
+    return [_REGISTRY[op] for op in ops]
+
+
+def _loaded_identities() -> set:
+    return {c.identity[:2] for c in _REGISTRY.values()}
+
+
+# ── the op group ──────────────────────────────────────────────────────────────
 
 class FAOps:
     """The ``fa`` op group (reference ``FAOps``, recsys.py:165-202)."""
 
     namespace = fa.NAMESPACE
     so_name = "libmi355_fa"
-    required_ops = [fa.OP_NAME]
-    fake_ops = [fa.OP_NAME]
-    op_schemas = {fa.OP_NAME: fa.SCHEMA}
-    build_version = "1"
-    default_offload_arch = "gfx950"
+    ops = {fa.OP_NAME: fa.SCHEMA}
+    meta_ops = (fa.OP_NAME,)
+    default_targets = ("gfx950",)
 
     def __init__(self, *, allow_jit: bool = True) -> None:
-        self._loaded = False
-        self._load_error: Optional[str] = None
-        self._library_path: Optional[Path] = None
-        self._metadata_path: Optional[Path] = None
         self._allow_jit = True
+        self._library: Optional[Path] = None
+        self._sidecar: Optional[Path] = None
+        self._error: Optional[str] = None
         self.configure(allow_jit=allow_jit)
 
-    # ── policy ──────────────────────────────────────────────────────────────
+    # policy
     @property
     def allow_jit(self) -> bool:
         """Whether load() may compile the in-tree library (hipcc)."""
@@ -164,279 +267,193 @@ class FAOps:
     def configure(self, *, allow_jit: bool) -> "FAOps":
         if not isinstance(allow_jit, bool):
             raise TypeError("allow_jit must be a bool")
-        with _LOCK:
-            self._allow_jit = allow_jit
+        self._allow_jit = allow_jit
         return self
 
     def disable_jit(self) -> "FAOps":
         return self.configure(allow_jit=False)
 
+    # state
     @property
     def library_path(self) -> Optional[Path]:
-        return self._library_path if self._loaded else None
+        return self._library
 
     @property
     def metadata_path(self) -> Optional[Path]:
-        return self._metadata_path if self._loaded else None
+        return self._sidecar
 
     def is_available(self) -> bool:
-        return self._loaded
+        return self._library is not None
 
     def load_error(self) -> Optional[str]:
-        return self._load_error
+        return self._error
 
-    # ── offline build ───────────────────────────────────────────────────────
-    def _schema_contract(self) -> dict:
-        return {f"{self.namespace}::{k}": f"{self.namespace}::{v}"
-                for k, v in sorted(self.op_schemas.items())}
+    # contract
+    def _qualified(self) -> list:
+        return sorted(f"{self.namespace}::{op}" for op in self.ops)
 
-    def _build_inputs(self, offload_arch, extra_flags) -> dict:
-        archs = _canonical_archs(offload_arch or self.default_offload_arch)
-        if not archs:
-            raise CustomOpsError("no offload target given")
-        flags = [f for f in _build.HIPCC_FLAGS if not f.startswith("--offload-arch=")]
-        extra = list(extra_flags)
-        for f in extra:
-            if not isinstance(f, str) or not f.strip() or "\n" in f:
-                raise CustomOpsError(f"invalid extra flag {f!r}")
-        return {"offload_arch": archs, "flags": flags, "extra_flags": extra,
-                "sources": [os.path.relpath(_build.SRC, _build.REPO_DIR)],
-                "include_dirs": [os.path.relpath(_build.INCLUDE, _build.REPO_DIR)]}
+    def contract(self) -> dict:
+        return {"namespace": self.namespace,
+                "schemas": {f"{self.namespace}::{op}": f"{self.namespace}::{schema}"
+                            for op, schema in sorted(self.ops.items())},
+                "meta_ops": sorted(self.meta_ops),
+                "abi": _lib.ABI_VERSION,
+                "group_version": GROUP_VERSION}
 
-    @staticmethod
-    def _source_fingerprint(inputs: dict) -> str:
-        h = hashlib.sha256(json.dumps(inputs, sort_keys=True).encode())
-        for rel in inputs["sources"]:
-            h.update(Path(_build.REPO_DIR, rel).read_bytes())
-        for rel in inputs["include_dirs"]:
-            for hdr in sorted(Path(_build.REPO_DIR, rel).glob("*.h")):
-                h.update(hdr.name.encode())
-                h.update(hdr.read_bytes())
-        return h.hexdigest()
+    def _expectation(self) -> _Expectation:
+        return _Expectation(self.contract(), _runtime_section(), frozenset(_visible_archs()))
+
+    # offline build
+    def _provenance(self, targets: list, extra: list) -> dict:
+        h = hashlib.sha256()
+        for src in [Path(_build.SRC), *sorted(Path(_build.INCLUDE).glob("*.h"))]:
+            h.update(src.name.encode() + b"\0" + src.read_bytes())
+        flags = [f for f in _build.HIPCC_FLAGS if not f.startswith("--offload-arch=")] + extra
+        try:
+            ver = subprocess.run([_build.hipcc(), "--version"], capture_output=True, text=True,
+                                 timeout=60).stdout.strip().splitlines()
+        except (OSError, subprocess.SubprocessError):
+            ver = []
+        return {"sources_sha256": h.hexdigest(), "flags": flags,
+                "compiler": next((l for l in ver if "version" in l.lower()), "")}
 
     def build(self, output_directory, *, offload_arch: Optional[str] = None,
               extra_flags=(), verbose: bool = False) -> Path:
-        """Compile and export ``<so_name>.so`` + ``<so_name>.so.json`` without loading.
+        """Compile ``<so_name>.so`` for the targets and publish its sealed sidecar
+        ``<so_name>.so.json`` next to it, without loading it. hipcc
+        cross-compiles, so no GPU is needed. Deploy both files together."""
+        targets = _targets(offload_arch or list(self.default_targets))
+        if not targets:
+            raise CustomOpsError("no offload target given")
+        extra = []
+        for f in extra_flags:
+            if not isinstance(f, str) or not f.strip() or "\n" in f:
+                raise CustomOpsError(f"invalid extra flag {f!r}")
+            extra.append(f)
+        out = Path(output_directory).expanduser().resolve()
+        out.mkdir(parents=True, exist_ok=True)
+        library = out / f"{self.so_name}.so"
+        sidecar = Path(str(library) + ".json")
+        with _LOCK, open(out / f".{self.so_name}.build.lock", "a") as lockf:
+            fcntl.flock(lockf, fcntl.LOCK_EX)
+            try:
+                if library.exists() and (library.stat().st_dev, library.stat().st_ino) \
+                        in _loaded_identities():
+                    raise CustomOpsError(
+                        f"cannot overwrite a library loaded in this process: {library}")
+                before = self._provenance(targets, extra)
+                with tempfile.TemporaryDirectory(prefix=".build-", dir=out) as tmp:
+                    product = Path(tmp) / library.name
+                    try:   # compiles and checks the device assembly (isa_check)
+                        _build.compile_checked(
+                            str(product), [*before["flags"], *[f"--offload-arch={t}" for t in targets]],
+                            verbose=verbose)
+                    except RuntimeError as e:
+                        raise CustomOpsError(str(e)) from e
+                    if self._provenance(targets, extra) != before:
+                        raise CustomOpsError("sources changed during the build; nothing published")
+                    manifest = {"format": ARTIFACT_FORMAT, "contract": self.contract(),
+                                "runtime": _runtime_section(), "targets": targets,
+                                "provenance": before,
+                                "payload": {"file": library.name,
+                                            "bytes": product.stat().st_size,
+                                            "sha256": _digest_file(product)}}
+                    manifest["seal"] = seal_of(manifest)
+                    staged = Path(tmp) / "sidecar.json"
+                    staged.write_text(json.dumps(manifest, sort_keys=True, indent=2) + "\n")
+                    os.replace(product, library)
+                    os.replace(staged, sidecar)
+            finally:
+                fcntl.flock(lockf, fcntl.LOCK_UN)
+        return library
 
-        hipcc cross-compiles, so this runs on a host without a GPU. Both files
-        must be deployed together."""
-        with _LOCK:
-            inputs = self._build_inputs(offload_arch, extra_flags)
-            fingerprint = self._source_fingerprint(inputs)
-            hipcc = _build.hipcc()
-            out = Path(output_directory).expanduser().resolve()
-            out.mkdir(parents=True, exist_ok=True)
-            library = out / f"{self.so_name}.so"
-            sidecar = library.with_suffix(library.suffix + ".json")
-            metadata = {
-                "format_version": METADATA_VERSION,
-                "producer": PRODUCER,
-                "namespace": self.namespace,
-                "so_name": self.so_name,
-                "build_version": self.build_version,
-                "compatibility": _runtime_compatibility(),
-                "offload_arch": inputs["offload_arch"],
-                "required_ops": sorted(self.required_ops),
-                "fake_ops": sorted(self.fake_ops),
-                "schemas": self._schema_contract(),
-                "schema_fingerprint": _json_hash(self._schema_contract()),
-                "source_fingerprint": fingerprint,
-                "build": {**inputs, "toolchain": {"hipcc": _hipcc_version(hipcc)}},
-            }
-            metadata["build_fingerprint"] = _metadata_fingerprint(metadata)
-            with (out / f"{self.so_name}.lock").open("a") as lock:
-                fcntl.flock(lock, fcntl.LOCK_EX)
-                try:
-                    if library.exists() and any(
-                            rec["identity"][:2] == _file_stat(library)[:2]
-                            for rec in _LIBRARIES.values()):
-                        raise CustomOpsError(
-                            f"cannot overwrite a library loaded in this process: {library}")
-                    with tempfile.TemporaryDirectory(prefix=f".{self.so_name}-build-",
-                                                     dir=out) as work:
-                        product = Path(work) / library.name
-                        cmd = [hipcc, *inputs["flags"],
-                               *[f"--offload-arch={a}" for a in inputs["offload_arch"]],
-                               *inputs["extra_flags"],
-                               *[f"-I{Path(_build.REPO_DIR, d)}" for d in inputs["include_dirs"]],
-                               *[str(Path(_build.REPO_DIR, s)) for s in inputs["sources"]],
-                               "-o", str(product)]
-                        if verbose:
-                            print(" ".join(cmd), flush=True)
-                        res = subprocess.run(cmd, capture_output=True, text=True)
-                        if res.returncode != 0:
-                            raise CustomOpsError(f"hipcc failed ({res.returncode}):\n"
-                                                 f"{res.stderr[-4000:]}")
-                        if self._source_fingerprint(inputs) != fingerprint:
-                            raise CustomOpsError("sources changed during the build; nothing exported")
-                        metadata["library"] = {"filename": library.name,
-                                               "sha256": _file_sha256(product),
-                                               "size": product.stat().st_size}
-                        pending = Path(work) / "metadata.json"
-                        pending.write_text(json.dumps(metadata, sort_keys=True, indent=2) + "\n")
-                        os.replace(product, library)
-                        os.replace(pending, sidecar)
-                finally:
-                    fcntl.flock(lock, fcntl.LOCK_UN)
-            return library
-
-    # ── precompiled load ────────────────────────────────────────────────────
-    def _validate_metadata(self, library: Path, sidecar: Path) -> tuple:
+    # loading
+    def _validate(self, library: Path, sidecar: Path) -> None:
         try:
-            metadata = json.loads(sidecar.read_text())
+            md = json.loads(sidecar.read_text())
         except (OSError, ValueError) as e:
-            raise CustomOpsError(f"unreadable metadata {sidecar}: {e}") from e
-        if not isinstance(metadata, dict):
-            raise CustomOpsError("precompiled metadata must be a JSON object")
-        expected = {"format_version": METADATA_VERSION, "producer": PRODUCER,
-                    "namespace": self.namespace, "so_name": self.so_name,
-                    "build_version": self.build_version}
-        for key, value in expected.items():
-            if metadata.get(key) != value or type(metadata.get(key)) is not type(value):
-                raise CustomOpsError(f"precompiled {key} mismatch: built={metadata.get(key)!r}, "
-                                     f"expected={value!r}")
-        compat = metadata.get("compatibility")
-        if not isinstance(compat, dict):
-            raise CustomOpsError("precompiled compatibility information is missing")
-        for key, value in _runtime_compatibility().items():
-            if compat.get(key) != value or type(compat.get(key)) is not type(value):
-                raise CustomOpsError(f"precompiled compatibility mismatch ({key}): "
-                                     f"built={compat.get(key)!r}, runtime={value!r}")
-        for key, ops in (("required_ops", self.required_ops), ("fake_ops", self.fake_ops)):
-            vals = metadata.get(key)
-            if not isinstance(vals, list) or sorted(vals) != sorted(ops):
-                raise CustomOpsError(f"precompiled {key} mismatch: built={vals}, "
-                                     f"expected={sorted(ops)}")
-        if metadata.get("schemas") != self._schema_contract():
-            raise CustomOpsError("precompiled schema contract does not match this Python wrapper")
-        if metadata.get("schema_fingerprint") != _json_hash(self._schema_contract()):
-            raise CustomOpsError("precompiled schema fingerprint is invalid")
-        for key in ("source_fingerprint", "build_fingerprint"):
-            if not isinstance(metadata.get(key), str) or not re.fullmatch(r"[0-9a-f]{64}",
-                                                                         metadata[key]):
-                raise CustomOpsError(f"precompiled {key} is missing or invalid")
-        if metadata["build_fingerprint"] != _metadata_fingerprint(metadata):
-            raise CustomOpsError("precompiled build fingerprint is invalid")
-        targets = metadata.get("offload_arch")
-        if not isinstance(targets, list) or not targets or targets != _canonical_archs(targets):
-            raise CustomOpsError("precompiled offload targets are missing or noncanonical")
-        visible = _visible_archs()
-        if not visible.issubset(targets):
-            raise CustomOpsError(f"precompiled target mismatch: visible={sorted(visible)}, "
-                                 f"built={targets}")
-        binary = metadata.get("library")
-        if not isinstance(binary, dict) or binary.get("filename") != library.name:
-            raise CustomOpsError("precompiled library identity information is missing")
-        if type(binary.get("size")) is not int or binary["size"] <= 0:
-            raise CustomOpsError("precompiled library size is invalid")
-        identity, stat = _library_identity(library)
-        if binary.get("sha256") != identity[2] or binary["size"] != stat[2]:
-            raise CustomOpsError(f"precompiled library hash/size mismatch: {library}")
-        return metadata, identity, stat
+            raise CustomOpsError(f"cannot read sidecar {sidecar}: {e}") from e
+        if not isinstance(md, dict):
+            raise CustomOpsError(f"sidecar {sidecar} is not a JSON object")
+        exp = self._expectation()
+        for name, check in _CHECKS:
+            msg = check(md, exp, library)
+            if msg:
+                raise CustomOpsError(f"{name} check: {msg}")
 
-    def _operator_names(self) -> set:
-        return {f"{self.namespace}::{n}" for n in set(self.required_ops) | set(self.op_schemas)}
+    def _verify_registered(self) -> None:
+        for qualified, schema in self.contract()["schemas"].items():
+            got = _registered_schema(qualified)
+            if got != schema:
+                raise CustomOpsError(f"registered schema {got!r} differs from the contract {schema!r}")
+        for op in self.meta_ops:
+            if not torch._C._dispatch_has_kernel_for_dispatch_key(f"{self.namespace}::{op}", "Meta"):
+                raise CustomOpsError(f"no Meta (fake) kernel for {self.namespace}::{op}")
 
-    def _check_conflicts(self, identity: tuple, names: set) -> None:
-        for rec in _LIBRARIES.values():
-            if rec["identity"][:2] == identity[:2] and rec["identity"] != identity:
-                raise CustomOpsError("an already loaded library file was modified; "
-                                     "use a fresh process")
-        rec = _LIBRARIES.get(identity)
-        if rec is not None and rec["error"] is not None:
-            raise CustomOpsError("this library previously failed after loading started; use a "
-                                 "fresh process. " + rec["error"])
-        for name in names:
-            owner = _OP_OWNERS.get(name)
-            if owner is not None and owner != identity:
-                raise CustomOpsError(f"dispatcher library conflict for {name}: already owned by "
-                                     f"{_LIBRARIES[owner]['path']}; use a fresh process")
-            if owner is None and _has_schema(name):
-                raise CustomOpsError(f"dispatcher operator {name} is already registered by an "
-                                     "untracked library; use a fresh process")
-
-    def _open(self, library: Path, identity: tuple) -> dict:
-        names = self._operator_names()
-        self._check_conflicts(identity, names)
-        rec = _LIBRARIES.get(identity)
-        if rec is not None and rec["ready"]:
-            return rec
-        rec = {"identity": identity, "path": library, "names": names, "ready": False,
-               "error": None}
-        _LIBRARIES[identity] = rec          # reserve before opening
-        for name in names:
-            _OP_OWNERS[name] = identity
+    def _bind(self, library: Path, prevalidated: Callable[[], None]) -> None:
+        """Claim the operators, open the library, register and verify, in that order."""
+        prevalidated()
+        identity = _identity(library)
+        claims = _claim(self._qualified(), library, identity)
+        if all(c.state == "live" for c in claims):
+            return
         try:
             _lib.load(str(library))
             fa.register()
+            self._verify_registered()
         except Exception as e:
-            rec["error"] = str(e)
+            for c in claims:
+                c.state, c.reason = "broken", str(e)
             raise
-        return rec
-
-    def _finish(self, rec: dict) -> None:
-        for name, schema in self._schema_contract().items():
-            got = _schema(name)
-            if got != schema:
-                rec["error"] = f"registered schema {got!r} != contract {schema!r}"
-                raise CustomOpsError(rec["error"])
-        for op in self.fake_ops:
-            if not torch._C._dispatch_has_kernel_for_dispatch_key(f"{self.namespace}::{op}",
-                                                                   "Meta"):
-                rec["error"] = f"fake/Meta implementation missing for {self.namespace}::{op}"
-                raise CustomOpsError(rec["error"])
-        rec["ready"] = True
-        self._library_path = rec["path"]
-        self._load_error = None
-        self._loaded = True
+        for c in claims:
+            c.state = "live"
 
     def load_precompiled(self, library_path, metadata_path=None) -> "FAOps":
-        """Validate, then load a deployment library; disables implicit compiling.
-
-        The default sidecar is ``<library_path>.json``."""
+        """Validate a deployed library and its sidecar (default ``<library>.json``),
+        then load it. Switches this group to strict mode (no compiling)."""
         with _LOCK:
             self._allow_jit = False
-            self._loaded = False
+            self._library = None
             try:
                 library = Path(library_path).expanduser().resolve(strict=True)
                 if not library.is_file():
-                    raise CustomOpsError(f"precompiled library is not a file: {library}")
-                sidecar = (Path(metadata_path).expanduser() if metadata_path is not None
-                           else Path(str(Path(library_path).expanduser()) + ".json"))
-                sidecar = sidecar.resolve(strict=True)
-                _, identity, stat = self._validate_metadata(library, sidecar)
-                if _file_stat(library) != stat:
-                    raise CustomOpsError(f"library changed during validation: {library}")
-                rec = self._open(library, identity)
-                self._finish(rec)
-                self._metadata_path = sidecar
+                    raise CustomOpsError(f"not a file: {library}")
+                sidecar = Path(metadata_path if metadata_path is not None
+                               else str(Path(library_path).expanduser()) + ".json")
+                sidecar = sidecar.expanduser().resolve(strict=True)
+                self._validate(library, sidecar)
+                stamp = library.stat()
+
+                def unchanged():
+                    now = library.stat()
+                    if (now.st_ino, now.st_size, now.st_mtime_ns) != \
+                            (stamp.st_ino, stamp.st_size, stamp.st_mtime_ns):
+                        raise CustomOpsError(f"{library} changed while it was being validated")
+                self._bind(library, unchanged)
+                self._library, self._sidecar, self._error = library, sidecar, None
             except Exception as e:
-                self._loaded = False
-                self._load_error = str(e)
+                self._error = str(e)
                 raise CustomOpsError(f"[FAOps] precompiled load failed (JIT disabled): {e}") from e
         return self
 
-    # ── development load ────────────────────────────────────────────────────
     def load(self) -> "FAOps":
-        """In-tree library; compiled with hipcc when missing and allow_jit is True."""
+        """Development path: the in-tree library, compiled with hipcc when it is
+        missing and ``allow_jit`` is True."""
         with _LOCK:
-            if self._loaded:
+            if self._library is not None:
                 return self
             if not self._allow_jit:
-                self._load_error = ("JIT is disabled for FAOps; call load_precompiled("
-                                    "library_path, metadata_path=None) before load()")
-                raise CustomOpsError(self._load_error)
+                self._error = ("JIT is disabled for FAOps; call load_precompiled("
+                               "library_path, metadata_path=None) before load()")
+                raise CustomOpsError(self._error)
             try:
                 path = Path(_build.lib_path())
                 if not path.exists():
                     _build.build()
                 path = path.resolve(strict=True)
-                identity, _ = _library_identity(path)
-                rec = self._open(path, identity)
-                self._finish(rec)
-                self._metadata_path = None
+                self._bind(path, lambda: None)
+                self._library, self._sidecar, self._error = path, None, None
             except Exception as e:
-                self._loaded = False
-                self._load_error = str(e)
+                self._error = str(e)
                 raise CustomOpsError(f"[FAOps] load failed: {e}") from e
         return self

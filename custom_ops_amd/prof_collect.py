@@ -9,6 +9,9 @@ never touches the GPU itself):
   3. --pmc WRITE_SIZE                HBM write KiB per dispatch
   4. --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_MFMA GRBM_GUI_ACTIVE
   5. --pmc SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_LDS GRBM_GUI_ACTIVE
+  6. --pmc FETCH_SIZE with the mask's strides set to 0 (prof_workload
+     --mask-bcast): the FETCH_SIZE difference against pass 2 is the HBM
+     traffic of the mask stream, which gives its counted GB/s
 The workload (custom_ops_amd.prof_workload) first runs y = 2·x over a 512 MiB
 fp32 buffer (5 dispatches of one elementwise kernel that reads and writes
 512 MiB each); its FETCH_SIZE / WRITE_SIZE against the known 512 MiB give the
@@ -38,17 +41,18 @@ PASSES = {
              "GRBM_GUI_ACTIVE"],
     "lds": ["--pmc", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS",
             "GRBM_GUI_ACTIVE"],
+    "fetch_bcast": ["--pmc", "FETCH_SIZE"],
 }
 
 
-def workload_cmd(cfg: str, iters: int) -> list[str]:
+def workload_cmd(cfg: str, iters: int, bcast: bool = False) -> list[str]:
     return [sys.executable, "-m", "custom_ops_amd.prof_workload", "--config", cfg, "--iters",
-            str(iters), "--copy-mib", str(COPY_MIB)]
+            str(iters), "--copy-mib", str(COPY_MIB), *(["--mask-bcast"] if bcast else [])]
 
 
 def rocprof_cmd(name: str, outdir: str, cfg: str, iters: int) -> list[str]:
     return ["rocprofv3", *PASSES[name], "--output-format", "csv", "-d", outdir, "--",
-            *workload_cmd(cfg, iters)]
+            *workload_cmd(cfg, iters, bcast=name.endswith("_bcast"))]
 
 
 def run_pass(name: str, outdir: str, cfg: str, iters: int) -> str:
@@ -131,6 +135,9 @@ def main() -> None:
     traffic = None
     if f_fac and w_fac:
         traffic = (fetch * f_fac + write * w_fac) * 1024
+    fetch_b = counter_means(dirs["fetch_bcast"], is_attn)["FETCH_SIZE"]
+    mask_alg = cfg.B * cfg.Sq * cfg.Sk * 2
+    mask_counted = (fetch - fetch_b) * f_fac * 1024 if f_fac else None
     mf = counter_means(dirs["mfma"], is_attn)
     ld = counter_means(dirs["lds"], is_attn)
     simds, xcds = 256 * 4, 8
@@ -159,6 +166,9 @@ def main() -> None:
         "algorithmic_bytes_per_launch": cfg.algorithmic_bytes,
         "hbm_gbps": traffic / (avg_ns * 1e-9) / 1e9 if traffic else None,
         "mask_stream_gbps_algorithmic": mask_bytes / (avg_ns * 1e-9) / 1e9,
+        "fetch_kib_raw_mask_bcast": fetch_b,
+        "mask_hbm_bytes_counted": mask_counted,
+        "mask_hbm_gbps_counted": mask_counted / (avg_ns * 1e-9) / 1e9 if mask_counted else None,
         "mfma_busy_pct": mfma_util,
         "active_cycles_per_xcd": gui,
         "clock_ghz_under_counters": gui / (avg_ns * 1e-9) / 1e9,
@@ -174,6 +184,16 @@ def main() -> None:
                    "hbm_bytes_per_launch": traffic,
                    "fetch_factor": f_fac, "write_factor": w_fac,
                    "avg_duration_us": avg_ns / 1e3}, f, indent=1)
+    with open(os.path.join(args.out, f"mask_stream_{stem}.json"), "w") as f:
+        json.dump({"config": cfg.name, "kernel": kname,
+                   "mask_bytes_algorithmic": mask_alg,
+                   "mask_hbm_bytes_counted": mask_counted,
+                   "mask_hbm_gbps_counted": (mask_counted / (avg_ns * 1e-9) / 1e9
+                                             if mask_counted else None),
+                   "fetch_kib_raw": fetch, "fetch_kib_raw_mask_bcast": fetch_b,
+                   "fetch_factor": f_fac, "avg_duration_us": avg_ns / 1e3,
+                   "source": "rocprofv3 FETCH_SIZE, normal call minus the same call with mask "
+                             "strides 0 (custom_ops_amd.prof_collect)"}, f, indent=1)
     lines = [f"# rocprofv3 summary: fa_fwd_kernel on {cfg.name}", ""]
     lines.append(f"workload: {cfg.name} B={cfg.B} H={cfg.H} Hk={cfg.Hk} Sq={cfg.Sq} Sk={cfg.Sk} "
                  f"d={cfg.d} bf16 ({cfg.description}); {args.iters} launches after clock settle")

@@ -3,6 +3,13 @@ configuration, optionally preceded by a plain device copy of known size (the
 calibration kernel for the FETCH_SIZE / WRITE_SIZE counters).
 
     python -m custom_ops_amd.prof_workload --config cfg2 --iters 20 [--copy-mib 512]
+        [--mask-bcast]
+
+--mask-bcast launches the same call through the C ABI with the mask's row and
+batch strides set to 0: every query row then reads the same (L2-resident)
+mask row, so the difference in FETCH_SIZE against the normal call is the
+mask stream's HBM traffic. The arithmetic is the same; only the mask values
+differ (no tile of the cfg2/cfg3 masks is entirely -inf either way).
 
 Inputs are generated and copied to the GPU before any timed launch; the GPU
 clocks are settled first with untimed launches (--settle-s).
@@ -18,6 +25,8 @@ def main() -> None:
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--settle-s", type=float, default=0.3)
+    ap.add_argument("--mask-bcast", action="store_true",
+                    help="mask row/batch strides 0: one L2-resident mask row for every query row")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run 5 copies of a buffer of this many MiB (read N, write N)")
     args = ap.parse_args()
@@ -38,13 +47,26 @@ def main() -> None:
         del src, dst
     cfg = CONFIGS[args.config]
     q, k, v, m = (t.to(dev) for t in make_inputs(cfg))
+    call = lambda: ops.mha_fwd_with_mask(q, k, v, m)  # noqa: E731
+    if args.mask_bcast:
+        from custom_ops_amd import _lib, fa
+        out = torch.empty_like(q)
+        p = fa.make_params(q, k, v, m, out)
+        p.mask_row_stride = 0
+        p.mask_batch_stride = 0
+        ws_bytes = _lib.workspace_bytes(p)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        if ws_bytes:
+            p.workspace, p.workspace_bytes = ws.data_ptr(), ws_bytes
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        call = lambda: _lib.fwd(p, stream)  # noqa: E731
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < args.settle_s:
         for _ in range(10):
-            ops.mha_fwd_with_mask(q, k, v, m)
+            call()
         torch.cuda.synchronize()
     for _ in range(args.iters):
-        ops.mha_fwd_with_mask(q, k, v, m)
+        call()
     torch.cuda.synchronize()
     print(f"prof_workload {cfg.name}: {args.iters} launches done", flush=True)
 

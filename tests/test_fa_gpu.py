@@ -598,3 +598,22 @@ def test_random_fuzz_vs_reference(ops, gpu):
         dead = torch.isinf(m[:, :, :sq, :sk].float()).all(-1).squeeze(1)   # [b, sq]
         if dead.any():
             assert torch.all(out.permute(0, 2, 1, 3)[dead] == 0), str(case)
+
+
+@pytest.mark.parametrize("shape", [(1, 16, 128, 32768, 128), (4, 16, 2048, 2048, 128),
+                                   (2, 16, 1000, 4099, 128), (1, 4, 64, 777, 64)])
+def test_num_splits_for_matches_library_plan(gpu, shape):
+    """fa.num_splits_for reports the split count the launcher plans (it is the
+    same C entry point, fed from the tensors)."""
+    from custom_ops_amd import _lib, fa
+    b, h, sq, sk, d = shape
+    q = torch.zeros(b, h, sq, d, dtype=torch.bfloat16, device=gpu)
+    k = torch.zeros(b, h, sk, d, dtype=torch.bfloat16, device=gpu)
+    m = torch.zeros(b, 1, sq, sk, dtype=torch.bfloat16, device=gpu)
+    got = fa.num_splits_for(q, k, k, m)
+    p = fa.make_params(q, k, k, m, torch.empty_like(q))
+    assert got == _lib.num_splits(p) >= 1
+    if shape[3] == 32768:
+        assert got > 1          # the small-grid long-Sk shape is split
+    if shape[0] == 4:
+        assert got == 1         # a grid that fills the chip is not

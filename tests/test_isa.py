@@ -1,22 +1,15 @@
 """CPU checks on the gfx950 assembly of this build's own kernels (hipcc
-cross-compiles without a GPU). They pin properties the GPU tests cannot see
-directly and that a compiler or source change can silently break:
-
-* M0 is written only inside the inline-assembly LDS DMA (which names it as a
-  clobber): the compiler must not keep a value of its own in M0 across it;
-* no packed-FP32 arithmetic (the build disables it);
-* no register spills and no scratch memory in any kernel (a kernel that fell
-  back to scratch ran 16x slower while still passing every numeric test).
+cross-compiles without a GPU), through the same checker every build runs
+(custom_ops_amd/isa_check.py): M0 only inside the LDS-DMA inline assembly, no
+packed FP32, no spills or scratch. Also pins that the checker itself catches
+each kind of violation, so a build that breaks them cannot be installed.
 """
-import os
-import re
 import subprocess
 
 import pytest
 
 from custom_ops_amd import build
-
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+from custom_ops_amd.isa_check import code_outside_asm, kernel_metadata, violations
 
 
 @pytest.fixture(scope="module")
@@ -30,48 +23,44 @@ def isa(tmp_path_factory):
     return out.read_text()
 
 
-def _code_outside_asm(text):
-    inside = False
-    for line in text.splitlines():
-        if ";;#ASMSTART" in line:
-            inside = True
-            continue
-        if ";;#ASMEND" in line:
-            inside = False
-            continue
-        code = line.split(";", 1)[0].strip()
-        if not inside and code:
-            yield code
+def test_build_assembly_is_clean(isa):
+    assert violations(isa) == []
 
 
-def _kernel_metadata(text):
-    """(name, {field: value}) for every kernel in the code-object metadata."""
-    meta = text[text.index("amdhsa.kernels:"):]
-    for block in meta.split("\n  - ")[1:]:
-        name = re.search(r"\.name:\s+(\S+)", block)
-        if not name:
-            continue
-        fields = dict(re.findall(r"\.(\w+):\s+(\d+)\s*$", block, re.M))
-        yield name.group(1), fields
+def test_every_variant_present(isa):
+    kernels = [k for k, _ in kernel_metadata(isa)]
+    assert len(kernels) >= 40, kernels
 
 
 def test_m0_only_inside_the_lds_dma_asm(isa):
-    assert ";;#ASMSTART" in isa, "the LDS DMA inline assembly is missing"
-    offenders = [c for c in _code_outside_asm(isa) if re.search(r"\bm0\b", c)]
-    assert not offenders, offenders[:10]
+    assert ";;#ASMSTART" in isa
+    assert not [c for c in code_outside_asm(isa) if "m0" in c.split()]
 
 
-def test_no_packed_fp32_arithmetic(isa):
-    offenders = [c for c in _code_outside_asm(isa)
-                 if re.match(r"v_pk_(add|mul|fma)_f32\b", c)]
-    assert not offenders, offenders[:10]
+_FAKE = """\
+\t;;#ASMSTART
+\ts_mov_b32 m0, s1
+\tbuffer_load_dwordx4 v1, s[4:7], 0 offen lds
+\t;;#ASMEND
+{body}
+amdhsa.kernels:
+  - .name:           k
+    .private_segment_fixed_size: {scratch}
+    .sgpr_spill_count: 0
+    .vgpr_spill_count: {spill}
+"""
 
 
-def test_no_spills_or_scratch(isa):
-    kernels = list(_kernel_metadata(isa))
-    assert len(kernels) >= 40, [k for k, _ in kernels]
-    bad = {name: f for name, f in kernels
-           if int(f.get("vgpr_spill_count", 0)) or int(f.get("sgpr_spill_count", 0))
-           or int(f.get("private_segment_fixed_size", 0))}
-    assert not bad, bad
-    assert "scratch_" not in isa
+@pytest.mark.parametrize("body,scratch,spill,expect", [
+    ("\tv_add_f32 v1, v2, v3", 0, 0, None),
+    ("\ts_mov_b32 m0, s2", 0, 0, "M0 used outside"),
+    ("\tv_pk_fma_f32 v[0:1], v[2:3], v[4:5], v[6:7]", 0, 0, "packed FP32"),
+    ("\tv_add_f32 v1, v2, v3", 16, 0, "spills or scratch"),
+    ("\tv_add_f32 v1, v2, v3", 0, 3, "spills or scratch"),
+])
+def test_checker_catches_each_violation(body, scratch, spill, expect):
+    found = violations(_FAKE.format(body=body, scratch=scratch, spill=spill))
+    if expect is None:
+        assert found == []
+    else:
+        assert any(expect in v for v in found), found

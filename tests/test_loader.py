@@ -43,20 +43,25 @@ def copy_pair(lib, dst_dir):
     return dst
 
 
-def test_build_exports_library_and_sidecar_without_loading(exported):
+def test_build_exports_library_and_sealed_sidecar_without_loading(exported):
     from custom_ops_amd import _lib
-    from custom_ops_amd.loader import _file_sha256
+    from custom_ops_amd.loader import ARTIFACT_FORMAT, _digest_file, seal_of
     md = json.loads(open(str(exported) + ".json").read())
-    assert md["producer"] == "custom_ops_amd" and md["namespace"] == "recsys_ops"
-    assert md["offload_arch"] == ["gfx950"]
-    assert md["schemas"] == {"recsys_ops::mha_fwd_with_mask":
-                             "recsys_ops::mha_fwd_with_mask(Tensor q, Tensor k, Tensor v, "
-                             "Tensor mask) -> Tensor"}
-    assert md["library"]["sha256"] == _file_sha256(exported)
-    assert md["library"]["size"] == exported.stat().st_size
-    assert md["compatibility"]["abi_version"] == _lib.ABI_VERSION
-    assert "-packed-fp32-ops" in md["build"]["flags"]
-    assert len(md["source_fingerprint"]) == 64 and len(md["build_fingerprint"]) == 64
+    assert md["format"] == ARTIFACT_FORMAT
+    assert md["contract"]["namespace"] == "recsys_ops"
+    assert md["targets"] == ["gfx950"]
+    assert md["contract"]["schemas"] == {
+        "recsys_ops::mha_fwd_with_mask":
+        "recsys_ops::mha_fwd_with_mask(Tensor q, Tensor k, Tensor v, Tensor mask) -> Tensor"}
+    assert md["contract"]["meta_ops"] == ["mha_fwd_with_mask"]
+    assert md["contract"]["abi"] == _lib.ABI_VERSION
+    assert md["payload"] == {"file": exported.name, "bytes": exported.stat().st_size,
+                             "sha256": _digest_file(exported)}
+    assert "-packed-fp32-ops" in md["provenance"]["flags"]
+    assert len(md["provenance"]["sources_sha256"]) == 64
+    assert md["seal"] == seal_of(md)
+    # the in-process library is untouched: building never loads
+    assert _lib.loaded_path() is None or "export" not in _lib.loaded_path()
 
 
 def test_precompiled_load_in_fresh_process_is_strict(exported):
@@ -100,18 +105,22 @@ def test_strict_facade_never_compiles_or_opens_the_dev_library():
     assert rc == 0 and "OK" in out, err[-3000:]
 
 
-@pytest.mark.parametrize("field,value,msg", [
-    ("namespace", "other_ops", "namespace mismatch"),
-    ("format_version", 99, "format_version mismatch"),
-    ("build_version", 1, "build_version mismatch"),
-    ("required_ops", ["mha_fwd"], "required_ops mismatch"),
-    ("offload_arch", ["gfx942", "gfx950"], "build fingerprint"),
+@pytest.mark.parametrize("path,value,msg", [
+    (("contract", "namespace"), "other_ops", "seal is broken"),
+    (("format",), "custom_ops_amd.artifact/1", "format mismatch"),
+    (("contract", "group_version"), "2", "seal is broken"),
+    (("targets",), ["gfx942", "gfx950"], "seal is broken"),
+    (("payload", "bytes"), 1, "seal is broken"),
 ])
-def test_metadata_mismatch_rejected_before_open(exported, tmp_path, field, value, msg):
+def test_edited_sidecar_rejected_before_open(exported, tmp_path, path, value, msg):
+    """An edited sidecar (seal not recomputed) never gets as far as dlopen."""
     lib = copy_pair(exported, tmp_path / "m")
     side = str(lib) + ".json"
     md = json.loads(open(side).read())
-    md[field] = value
+    node = md
+    for key in path[:-1]:
+        node = node[key]
+    node[path[-1]] = value
     open(side, "w").write(json.dumps(md))
     rc, out, err = run_py(f"""
         from custom_ops_amd.loader import FAOps, CustomOpsError
@@ -125,26 +134,26 @@ def test_metadata_mismatch_rejected_before_open(exported, tmp_path, field, value
     assert rc == 0 and "ERR" in out and msg in out, (out, err[-2000:])
 
 
-def test_schema_contract_and_compat_mismatch(exported, tmp_path):
-    from custom_ops_amd.loader import _metadata_fingerprint
-    for field, mutate, msg in [
-        ("schemas", lambda md: md["schemas"].update(
+def test_resealed_mismatches_name_the_section(exported, tmp_path):
+    """A consistently resealed but wrong sidecar fails on the section that differs."""
+    from custom_ops_amd.loader import CustomOpsError, FAOps, seal_of
+    for i, (mutate, msg) in enumerate([
+        (lambda md: md["contract"]["schemas"].update(
             {"recsys_ops::mha_fwd_with_mask": "recsys_ops::mha_fwd_with_mask(Tensor q) -> Tensor"}),
-         "schema contract"),
-        ("compatibility", lambda md: md["compatibility"].update({"abi_version": 2}),
-         "compatibility mismatch (abi_version)"),
-        ("compatibility", lambda md: md["compatibility"].update({"torch": "1.13"}),
-         "compatibility mismatch (torch)"),
-        ("offload_arch", lambda md: md.update({"offload_arch": ["GFX950"]}), "invalid offload"),
-    ]:
-        lib = copy_pair(exported, tmp_path / field / msg[:8].replace(" ", "_"))
+         "contract mismatch (schemas"),
+        (lambda md: md["contract"].update({"namespace": "other_ops"}), "contract mismatch (namespace"),
+        (lambda md: md["contract"].update({"abi": 2}), "contract mismatch (abi"),
+        (lambda md: md["runtime"].update({"torch": "1.13"}), "runtime mismatch (torch"),
+        (lambda md: md.update({"targets": ["GFX950"]}), "invalid offload target"),
+        (lambda md: md["payload"].update({"bytes": 1}), "payload size mismatch"),
+    ]):
+        lib = copy_pair(exported, tmp_path / f"case{i}")
         side = str(lib) + ".json"
         md = json.loads(open(side).read())
         mutate(md)
-        md["build_fingerprint"] = _metadata_fingerprint(md)   # a consistent but wrong sidecar
+        md["seal"] = seal_of(md)
         open(side, "w").write(json.dumps(md))
-        from custom_ops_amd.loader import FAOps, CustomOpsError
-        with pytest.raises(CustomOpsError, match=msg.replace("(", r"\(").replace(")", r"\)")):
+        with pytest.raises(CustomOpsError, match=msg.replace("(", r"\(")):
             FAOps().load_precompiled(lib)
 
 
@@ -163,7 +172,7 @@ def test_modified_or_missing_files_rejected(exported, tmp_path):
         b = f.read(1)
         f.seek(4096)
         f.write(bytes([b[0] ^ 0xFF]))
-    with pytest.raises(CustomOpsError, match="hash/size mismatch"):
+    with pytest.raises(CustomOpsError, match="payload digest mismatch"):
         FAOps().load_precompiled(lib)
     lib2 = copy_pair(exported, tmp_path / "n")
     os.remove(str(lib2) + ".json")
@@ -183,7 +192,7 @@ def test_copy_of_loaded_library_is_a_dispatcher_conflict(exported, tmp_path):
         except CustomOpsError as e:
             print("ERR", e)
     """)
-    assert rc == 0 and "dispatcher library conflict" in out, (out, err[-2000:])
+    assert rc == 0 and "cannot serve it in this process" in out, (out, err[-2000:])
 
 
 def test_untracked_registration_is_fail_closed(exported):
@@ -221,3 +230,27 @@ def test_policy_is_explicit_bool():
         with pytest.raises(TypeError):
             obj.configure(allow_jit="no")
         assert obj.disable_jit().allow_jit is False
+
+
+def test_failure_after_open_is_sticky(exported):
+    """A load that fails after the library was opened marks the operator broken:
+    retrying in the same process is refused instead of half-registering twice."""
+    rc, out, err = run_py(f"""
+        from custom_ops_amd import fa
+        from custom_ops_amd.loader import FAOps, CustomOpsError
+        orig = fa.register
+        def boom():
+            raise RuntimeError("injected registration failure")
+        fa.register = boom
+        try:
+            FAOps().load_precompiled({str(exported)!r})
+        except CustomOpsError as e:
+            print("ERR1", e)
+        fa.register = orig
+        try:
+            FAOps().load_precompiled({str(exported)!r})
+        except CustomOpsError as e:
+            print("ERR2", e)
+    """)
+    assert rc == 0 and "injected registration failure" in out, (out, err[-2000:])
+    assert "ERR2" in out and "failed midway" in out, (out, err[-2000:])
