@@ -312,6 +312,72 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int mask_swz(int m) { return (m >> 1) & 7; }
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
+// O (or a split's partial O) of 32 query rows, normalised by l and rounded to
+// the input dtype, leaves through LDS. In the MFMA layout a lane holds 4
+// consecutive d of one row per 16-byte chunk, so a direct store instruction
+// would touch 32 rows with 8 bytes each; re-read from LDS, a lane holds one
+// whole 16-byte chunk and a store instruction writes 64 / (D/8) consecutive
+// whole rows. Chunks are XOR-swizzled by row so the writes and re-reads are
+// free of bank conflicts. stg is the caller's own 32·D·2-byte LDS region,
+// which no other wave touches. l_run is this lane's partial row sum (the
+// lane 32 apart holds the rest), m_run the row's running max of
+// u = q·k + mask/scale.
+template <int D, bool BF16, bool SPLIT>
+__device__ __forceinline__ void write_rows(const KParams& p, const f32x16 (&oacc)[D / 32], float l_run,
+                                           float m_run, int b, int h, int split, int qrow, uint8_t* stg,
+                                           int lane) {
+  constexpr int DB = D / 32;
+  const int l32 = lane & 31, g = lane >> 5;
+  const float l = xhalf_sum(l_run);
+  const float inv = (l == 0.f || l != l) ? 1.f : 1.f / l;
+  constexpr int CH = D / 8;      // 16-byte chunks per row
+  constexpr int RPI = 64 / CH;   // rows per re-read instruction
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      f32x4 v4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
+      u32x2 packed;
+      if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
+      else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
+      const int c = db * 4 + q4;   // chunk of d = db·32 + q4·8 .. +7; this lane's half g
+      *reinterpret_cast<u32x2*>(stg + l32 * D * 2 + ((c ^ (l32 & (CH - 1))) * 16) + g * 8) = packed;
+    }
+  }
+  const int ch = lane % CH, r0 = lane / CH;
+  const int row0 = qrow - l32;   // the first of the 32 rows
+  if constexpr (!SPLIT) {
+    const rsrc_t ro = make_rsrc(p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs,
+                                (uint32_t)p.sq * p.o_rs * 2u);
+#pragma unroll
+    for (int k = 0; k < 32 / RPI; ++k) {
+      const int r = r0 + k * RPI;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
+      // rows at or past Sq fall outside the buffer and are dropped
+      __builtin_amdgcn_raw_buffer_store_b128(v, ro, (uint32_t)((row0 + r) * p.o_rs + ch * 8) * 2u, 0, 0);
+    }
+  } else {
+    // partial O normalised by the split's own l, rounded to the input
+    // dtype as the reference stores it (fa_fwd_launch.h:289-297)
+    const int64_t bh = (int64_t)b * p.h + h;
+    const int64_t slab = (int64_t)p.b * p.h * p.sq;
+    const int64_t pbase = (int64_t)split * slab + bh * p.sq;
+#pragma unroll
+    for (int k = 0; k < 32 / RPI; ++k) {
+      const int r = r0 + k * RPI;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
+      if (row0 + r < p.sq) *reinterpret_cast<u32x4*>(p.o_part + (pbase + row0 + r) * D + ch * 8) = v;
+    }
+    if (g == 0 && qrow < p.sq)
+      p.lse_part[pbase + qrow] = (l == 0.f || l != l) ? -INFINITY
+                                 : __builtin_fmaf(m_run, p.scale, __builtin_amdgcn_logf(l) * 0.69314718f);
+  }
+}
+
 template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
 struct Attn {
   typedef typename Elt<BF16>::v8 V8;
@@ -630,63 +696,8 @@ struct Attn {
     }
   }
 
-  // O (or a split's partial O) of the wave's 32 rows, normalised by l and
-  // rounded to the input dtype, leaves through LDS. In the MFMA layout a lane
-  // holds 4 consecutive d of one row per 16-byte chunk, so a direct store
-  // instruction would touch 32 rows with 8 bytes each; re-read from LDS, a
-  // lane holds one whole 16-byte chunk and a store instruction writes
-  // 64 / (D/8) consecutive whole rows. Chunks are XOR-swizzled by row so the
-  // writes and re-reads are free of bank conflicts. stg is this wave's own
-  // 32·D·2-byte LDS region, which no other wave touches.
   __device__ __forceinline__ void epilogue(int b, int h, int split, int qrow, uint8_t* stg) {
-    const float l = xhalf_sum(l_run);
-    const float inv = (l == 0.f || l != l) ? 1.f : 1.f / l;
-    constexpr int CH = D / 8;      // 16-byte chunks per row
-    constexpr int RPI = 64 / CH;   // rows per re-read instruction
-    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-    typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        f32x4 v4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = oacc[db][q4 * 4 + i] * inv;
-        u32x2 packed;
-        if constexpr (BF16) packed = bitcast<u32x2>(__builtin_convertvector(v4, bf16x4));
-        else packed = bitcast<u32x2>(__builtin_convertvector(v4, f16x4));
-        const int c = db * 4 + q4;   // chunk of d = db·32 + q4·8 .. +7; this lane's half g
-        *reinterpret_cast<u32x2*>(stg + l32 * D * 2 + ((c ^ (l32 & (CH - 1))) * 16) + g * 8) = packed;
-      }
-    }
-    const int ch = lane % CH, r0 = lane / CH;
-    const int row0 = qrow - l32;   // the wave's first row
-    if constexpr (!SPLIT) {
-      const rsrc_t ro = make_rsrc(p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs,
-                                  (uint32_t)p.sq * p.o_rs * 2u);
-#pragma unroll
-      for (int k = 0; k < 32 / RPI; ++k) {
-        const int r = r0 + k * RPI;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
-        // rows at or past Sq fall outside the buffer and are dropped
-        __builtin_amdgcn_raw_buffer_store_b128(v, ro, (uint32_t)((row0 + r) * p.o_rs + ch * 8) * 2u, 0, 0);
-      }
-    } else {
-      // partial O normalised by the split's own l, rounded to the input
-      // dtype as the reference stores it (fa_fwd_launch.h:289-297)
-      const int64_t bh = (int64_t)b * p.h + h;
-      const int64_t slab = (int64_t)p.b * p.h * p.sq;
-      const int64_t pbase = (int64_t)split * slab + bh * p.sq;
-#pragma unroll
-      for (int k = 0; k < 32 / RPI; ++k) {
-        const int r = r0 + k * RPI;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
-        if (row0 + r < p.sq) *reinterpret_cast<u32x4*>(p.o_part + (pbase + row0 + r) * D + ch * 8) = v;
-      }
-      if (g == 0 && qrow < p.sq)
-        p.lse_part[pbase + qrow] = (l == 0.f || l != l) ? -INFINITY
-                                   : __builtin_fmaf(m_run, p.scale, __builtin_amdgcn_logf(l) * 0.69314718f);
-    }
+    write_rows<D, BF16, SPLIT>(p, oacc, l_run, m_run, b, h, split, qrow, stg, lane);
   }
 };
 
@@ -832,6 +843,190 @@ void fa_fwd_kernel(const KParams p) {
   uint8_t* stg = (a.wave < 4 ? reinterpret_cast<uint8_t*>(&sK[0][0]) : reinterpret_cast<uint8_t*>(&sV[0][0]))
                  + (a.wave & 3) * 32 * D * 2;
   a.epilogue(ti.b, ti.h, ti.split, qrow, stg);
+}
+
+// ── software-pipelined tile loop in generated assembly (d = 128) ─────────────
+// fa_fwd_kernel_asm<NH>: workgroups of BM = 256 query rows (the 8-wave plan's
+// grid), each wave 32·NH rows as NH halves of 32:
+//   NH = 1: 8 waves, two per SIMD (256 registers each)
+//   NH = 2: 4 waves, one per SIMD (512 registers each; each K and V operand
+//           read from LDS then feeds two MFMAs)
+// Q and O live in AGPRs. The tile loop is one inline-assembly block generated
+// by gen_fa_loop.py (fa_loop.inc), which also emits the operand bindings. It
+// runs QK of tile n+1 and PV of tile n as one MFMA stream under the exponentials
+// and P conversion of tile n and the mask add, row max and rescale test of tile
+// n+1, with all LDS operand reads in one queue. K, V and the mask tile (the
+// wave's own rows) arrive by LDS DMA, two stages each, one barrier per tile.
+// bf16 masks are added on the matrix core (an MFMA whose A operand selects each
+// score's key with weight bf16(1/scale)); fp16 masks by v_fma_mix.
+// Masks must have 16-byte aligned rows (the LDS DMA path).
+#include "fa_loop.inc"
+
+constexpr int kAsmKStage = 16384;                           // K or V stage: 64 keys x 128 d x 2
+constexpr int kAsmMStage = 32768;                           // mask stage: 256 rows x 64 keys x 2
+constexpr int kAsmLds = 4 * kAsmKStage + 2 * kAsmMStage;    // 128 KiB
+constexpr int kAsmVBase = 2 * kAsmKStage;
+constexpr int kAsmMBase = 4 * kAsmKStage;
+
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
+template <int N> struct U32Vec;
+template <> struct U32Vec<2> { typedef u32x2 type; };
+template <> struct U32Vec<4> { typedef u32x4 type; };
+template <> struct U32Vec<8> { typedef u32x8 type; };
+
+template <int NH, bool BF16, bool SPLIT>
+__global__ __launch_bounds__(NH == 1 ? 512 : 256)
+__attribute__((amdgpu_waves_per_eu(NH == 1 ? 2 : 1, NH == 1 ? 2 : 1)))
+void fa_fwd_kernel_asm(const KParams p) {
+  constexpr int D = 128;
+  constexpr int UPR = D / 8;                       // 16-byte units per K/V row
+  constexpr int WAVES = NH == 1 ? 8 : 4;
+  constexpr int NKL = 16 / WAVES;                  // K (and V) DMA loads per wave per tile
+  constexpr int NML = 4 * NH;                      // mask DMA loads per wave per tile
+  constexpr int ROWS = 32 * NH;                    // query rows per wave
+  __shared__ __align__(16) uint8_t smem[kAsmLds];
+  const TileIdx ti = tile_index<256>(p);
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+
+  const uint16_t* kbase = p.k + (int64_t)ti.b * p.k_bs + (int64_t)ti.hk * p.k_hs;
+  const uint16_t* vbase = p.v + (int64_t)ti.b * p.v_bs + (int64_t)ti.hk * p.v_hs;
+  const uint16_t* mbase = p.mask + (int64_t)ti.b * p.m_bs;
+  const uint32_t kbytes = (uint32_t)p.sk * p.k_rs * 2u, vbytes = (uint32_t)p.sk * p.v_rs * 2u;
+  const uint32_t mbytes = (uint32_t)p.msq * p.m_rs * 2u;
+  const int nb = ti.nb, ne = ti.ne;
+  const int cnt = ne - nb;
+
+  // DMA sources: K rows permuted within 32-key blocks (a lane of the score
+  // tile then owns 16 consecutive keys), V in key order, this wave's mask rows
+  typename U32Vec<NKL>::type koff, voff;
+#pragma unroll
+  for (int i = 0; i < NKL; ++i) {
+    const int u = (i * WAVES + wave) * 64 + lane;
+    const int r = u / UPR, slot = u % UPR;
+    const int key = (r & ~31) + key_perm(r & 31);
+    koff[i] = (uint32_t)(key * p.k_rs + (slot ^ (r % UPR)) * 8) * 2u;
+    voff[i] = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
+  }
+  typename U32Vec<NML>::type moff;
+#pragma unroll
+  for (int i = 0; i < NML; ++i) {
+    const int m = i * 8 + lane / 8, slot = lane % 8;
+    moff[i] = (uint32_t)((ti.m0 + wave * ROWS + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
+  }
+  u32x8 krd;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) krd[i] = lds0 + (uint32_t)(l32 * UPR + ((2 * i + g) ^ (l32 % UPR))) * 16u;
+  u32x4 vrd, mrd;
+  {
+    const int s16 = lane & 15, grp = lane >> 4;
+    const int row = 16 * g + s16 / 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int d = 32 * db + 16 * (grp & 1) + 4 * (s16 & 3);
+      vrd[db] = lds0 + kAsmVBase + (uint32_t)(row * D * 2 + (((d / 8) ^ v_swz<D>(row)) * 16) + (d % 8) * 2);
+    }
+    // mask read i of block b = i / 2: bf16 reads chunk c = i % 2 (keys 16c + 8g ..
+    // +7, the B operand of a mask MFMA); fp16 reads the lane's own 16 keys
+    // 16g .. +15 as two 8-key units (widened by v_fma_mix). Half h adds 4096.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = BF16 ? 4 * (i / 2) + 2 * (i % 2) + g : 4 * (i / 2) + 2 * g + (i % 2);
+      mrd[i] = lds0 + kAsmMBase + (uint32_t)(wave * ROWS * 128 + l32 * 128 + ((c ^ mask_swz(l32)) * 16));
+    }
+  }
+  // bf16 mask selectors: A_c[row i][k] = bf16(1/scale) where key π(i) = 16c + k
+  // (this lane: row l32, k = 8g + e), else 0
+  u32x8 msel = {};
+  if constexpr (BF16) {
+    const uint32_t sb = (uint32_t)bitcast<uint16_t>((__bf16)(1.f / p.scale));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int e = key_perm(l32) - 16 * c - 8 * g;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) msel[4 * c + w] = (e == 2 * w) ? sb : (e == 2 * w + 1) ? (sb << 16) : 0u;
+    }
+  }
+  const uint32_t mclamp = __builtin_amdgcn_readfirstlane(0xff7fff7fu);   // -max_bf16 pair
+  // Q of every half (rows past Sq read 0)
+  const rsrc_t rq = make_rsrc(p.q + (int64_t)ti.b * p.q_bs + (int64_t)ti.h * p.q_hs,
+                              (uint32_t)p.sq * p.q_rs * 2u);
+  u32x32 q[NH];
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) {
+    const int qrow = ti.m0 + wave * ROWS + hh * 32 + l32;
+#pragma unroll
+    for (int kd = 0; kd < 8; ++kd) {
+      const u32x4 v = bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[hh][4 * kd + e] = v[e];
+    }
+  }
+  // With Sk % 64 != 0 the last tile's DMA leaves V rows unwritten: zero the
+  // V stages once so those rows hold finite values (their P is exactly 0).
+  if (p.sk % kBN != 0) {
+    for (int i = tid; i < 2 * kAsmKStage / 16; i += 64 * WAVES)
+      reinterpret_cast<u32x4*>(smem + kAsmVBase)[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  const uint32_t ksh = (uint32_t)nb * kBN * (uint32_t)p.k_rs * 2u;
+  const uint32_t vsh = (uint32_t)nb * kBN * (uint32_t)p.v_rs * 2u;
+  const uint32_t msh = (uint32_t)nb * kBN * 2u;
+  const uint64_t ka = reinterpret_cast<uint64_t>(kbase) + ksh;
+  const uint64_t va = reinterpret_cast<uint64_t>(vbase) + vsh;
+  const uint64_t ma = reinterpret_cast<uint64_t>(mbase) + msh;
+  // Integer scalars go through readfirstlane (SGPR operands). The float
+  // scalars, which the compiler computes in VGPRs, are bound to fixed VGPRs
+  // outside the loop's working set (handed to an "s" operand they arrive as
+  // whatever VGPR holds them, possibly inside the loop's register range).
+  auto sgpr = [](uint32_t x) { return __builtin_amdgcn_readfirstlane(x); };
+  const uint32_t klo = sgpr((uint32_t)ka), khi = sgpr((uint32_t)(ka >> 32) & 0xffffu);
+  const uint32_t kn = sgpr(kbytes - ksh);
+  const uint32_t vlo = sgpr((uint32_t)va), vhi = sgpr((uint32_t)(va >> 32) & 0xffffu);
+  const uint32_t vn = sgpr(vbytes - vsh);
+  const uint32_t mlo = sgpr((uint32_t)ma), mhi = sgpr((uint32_t)(ma >> 32) & 0xffffu);
+  const uint32_t mn = sgpr(mbytes - msh);
+  const uint32_t fl = sgpr((uint32_t)kRsrcFlags);
+  const uint32_t kstep = sgpr((uint32_t)kBN * p.k_rs * 2u);
+  const uint32_t vstep = sgpr((uint32_t)kBN * p.v_rs * 2u);
+  const uint32_t lds_k = sgpr(lds0 + (uint32_t)wave * 1024u);
+  const uint32_t lds_v = sgpr(lds0 + kAsmVBase + (uint32_t)wave * 1024u);
+  const uint32_t lds_m = sgpr(lds0 + kAsmMBase + (uint32_t)(wave * ROWS * 128));
+  const uint32_t lim = sgpr((ne == p.num_n && p.sk % kBN) ? (uint32_t)(p.sk % kBN) : 64u);
+  const float c2 = p.scale * kLog2e, inv_scale = 1.f / p.scale, slack = kRescaleSlack / p.scale;
+  const float neginf = -INFINITY;
+  const uint32_t ntiles = sgpr((uint32_t)cnt);
+
+  f32x16 o[4 * NH];
+  float mrun[NH], lsum[NH];
+  if (cnt > 0) {
+    if constexpr (NH == 2) {
+      if constexpr (BF16) asm volatile(MI355_W64_LOOP_BF16 : MI355_W64_OUTPUTS_BF16 : MI355_W64_INPUTS_BF16 : MI355_W64_CLOBBERS_BF16);
+      else asm volatile(MI355_W64_LOOP_F16 : MI355_W64_OUTPUTS_F16 : MI355_W64_INPUTS_F16 : MI355_W64_CLOBBERS_F16);
+    } else {
+      if constexpr (BF16) asm volatile(MI355_W32_LOOP_BF16 : MI355_W32_OUTPUTS_BF16 : MI355_W32_INPUTS_BF16 : MI355_W32_CLOBBERS_BF16);
+      else asm volatile(MI355_W32_LOOP_F16 : MI355_W32_OUTPUTS_F16 : MI355_W32_INPUTS_F16 : MI355_W32_CLOBBERS_F16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4 * NH; ++i) o[i] = f32x16{};
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) { mrun[hh] = -INFINITY; lsum[hh] = 0.f; }
+  }
+  // every wave is past its last LDS read and DMA: LDS becomes output staging
+  wait_vmcnt<0>();
+  wg_barrier();
+#pragma unroll
+  for (int hh = 0; hh < NH; ++hh) {
+    const f32x16 oh[4] = {o[4 * hh], o[4 * hh + 1], o[4 * hh + 2], o[4 * hh + 3]};
+    const int qrow = ti.m0 + wave * ROWS + hh * 32 + l32;
+    write_rows<D, BF16, SPLIT>(p, oh, lsum[hh], mrun[hh], ti.b, ti.h, ti.split, qrow,
+                               smem + (wave * NH + hh) * 8192, lane);
+  }
 }
 
 // ── split-KV combine ────────────────────────────────────────────────────────
@@ -1138,8 +1333,30 @@ static hipError_t launch_main(const KParams& kp, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The generated-loop kernel serves the 8-wave plans at d = 128 with 16-byte
+// aligned mask rows. MI355_FA_ASM selects its form: 1 (default) = 8 waves of
+// 32 rows, 2 = 4 waves of 64 rows, 0 = the compiled 8-wave kernel instead.
+static int asm_form() {
+  static const int f = [] {
+    const char* e = getenv("MI355_FA_ASM");
+    return (e && (e[0] == '0' || e[0] == '2')) ? e[0] - '0' : 1;
+  }();
+  return f;
+}
+
 template <int D, bool BF16, bool SPLIT>
 static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t st) {
+  if constexpr (D == 128) {
+    // bf16 adds the mask on the matrix core, which needs bf16(1/scale) > 1.0078
+    // (-max_bf16 · (1/scale) must overflow to -inf): scale < 0.99
+    if (pl.waves == 8 && kp.mask_direct && asm_form() && (!BF16 || kp.scale < 0.99f)) {
+      if (asm_form() == 2)
+        hipLaunchKernelGGL((fa_fwd_kernel_asm<2, BF16, SPLIT>), dim3(kp.total), dim3(256), 0, st, kp);
+      else
+        hipLaunchKernelGGL((fa_fwd_kernel_asm<1, BF16, SPLIT>), dim3(kp.total), dim3(512), 0, st, kp);
+      return hipGetLastError();
+    }
+  }
   return pl.waves == 8 ? launch_main<D, BF16, SPLIT, 8>(kp, st)
                        : launch_main<D, BF16, SPLIT, 4>(kp, st);
 }

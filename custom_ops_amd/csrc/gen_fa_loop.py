@@ -1,0 +1,814 @@
+#!/usr/bin/env python3
+"""Generate the gfx950 tile loop of the 64-rows-per-wave attention kernel.
+
+    python custom_ops_amd/csrc/gen_fa_loop.py   # rewrites fa_loop.inc
+
+The loop is emitted as GCN assembly text (one C++ string per element type) that
+``fa_fwd.hip`` places in a single inline-asm statement. Writing it out
+instruction by instruction fixes two things the compiler does not do for this
+loop: a software pipeline across KV tiles inside one wave, and an exact
+interleave of matrix-core (MFMA) and vector-ALU work.
+
+Work per wave: 64 query rows as two halves h = 0, 1 of 32 rows; KV tiles of 64
+keys. For tile n (S[n % 2] holds its scores u = q·k + mask/scale):
+
+  X(n): MFMA  S[(n+1) % 2] = K(n+1)·Qᵀ          (32 MFMAs, K from LDS)
+        VALU  P(n) = exp2(u·c2 - m·c2) -> bf16/fp16, in place in S[n % 2]
+  Y(n): MFMA  Oᵀ += Vᵀ(n)·Pᵀ(n)                 (32 MFMAs, V read transposed)
+        VALU  row sums of P(n); mask(n+1)/scale added to S[(n+1) % 2];
+              row max of tile n+1; lazy rescale decision
+
+so every MFMA of one phase runs under the VALU work of the other tile. Q and O
+live in AGPRs (MFMA operands and accumulators); the scores, operand windows and
+addresses in VGPRs. K, V and the mask tile arrive by LDS DMA (two stages each),
+one workgroup barrier per tile.
+
+Register map (physical, fixed by this generator; fa_fwd.hip binds its operands
+to the same registers):
+  v[0:63]    S0      (half h: v[32h .. 32h+31], block b: +16b)
+  v[64:127]  S1
+  v[128:143] K operand window, 4 slots
+  v[144:159] V operand window, 4 slots
+  v[160:175] mask window: fp16, 2 slots of 8 (two 16-byte LDS reads each);
+             bf16, 2 slots of 4 (v160..167) and the mask selectors (v168..175)
+  v[176:179] K DMA offsets    v[180:183] V DMA offsets   v[184:191] mask DMA offsets
+  v[192:199] K LDS read addresses (per 16-d step)        v[200:203] V read addresses
+  v[204:207] mask LDS read addresses
+  v208/209 running max (u units) of half 0/1   v210/211 max·c2   v212/213 row sums
+  v[214:223] temporaries, v224 -inf, v225..v228 c2, 1/scale, slack, -inf (inputs)
+  a[0:63]    Q (half h: a[32h + 4kd .. +3])     a[64:191] O (half h: a[64 + 64h + 16db ..])
+  s[80:83] K descriptor, s[84:87] V descriptor, s[88:91] mask descriptor,
+  s92 tile counter, s[94:97] ballots
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT = os.path.join(HERE, "fa_loop.inc")
+# Timing-only ablations (never used for the committed output): comma list of
+# noexp, novaluy, noqk, nopv, nodmam, nobar, nodma, nolds, ts (phase
+# timestamps into a debug buffer whose address the scratch build binds to
+# v[231:232])
+ABL = set(filter(None, os.environ.get("W64_ABLATE", "").split(",")))
+
+D = 128
+KD = D // 16          # 16-d steps of QK
+DB = D // 32          # 32-d blocks of O
+KSTAGE = 16384        # bytes per K (or V) stage: 64 keys x 128 d x 2
+MSTAGE = 32768        # bytes per mask stage: 256 rows x 64 keys x 2
+# LDS layout: [K stage 0|1][V stage 0|1][mask stage 0|1] = 128 KiB. The region
+# bases are folded into the address registers on the C side (ds_read immediate
+# offsets are 16-bit), so the offsets below are relative to each region.
+K_LDS = V_LDS = M_LDS = 0
+LDS_BYTES = 4 * KSTAGE + 2 * MSTAGE
+
+# Register map, set by configure(nh) for one of the two kernels:
+#   nh = 2: 4 waves of 64 rows (one wave per SIMD; 512 registers per wave)
+#   nh = 1: 8 waves of 32 rows (two waves per SIMD; 256 registers per wave)
+# Window bases stay multiples of 4 (MFMA operand tuples).
+def configure(nh):
+    g = globals()
+    g["NH"] = nh
+    g["WAVES"] = 8 if nh == 1 else 4
+    g["SBUF"] = 32 * nh                  # registers per score buffer
+    r = 2 * SBUF
+    g["KWIN"] = r; r += 16               # K operand window, 4 slots
+    g["VWIN"] = r; r += 16               # V operand window, 4 slots
+    g["MWIN"] = r; r += 8                # mask window, 2 slots of 4
+    g["MSEL"] = r; r += 8                # bf16 mask selectors A_0, A_1
+    g["NKL"] = 16 // WAVES               # K (and V) DMA loads per wave per tile
+    g["NML"] = 4 * nh                    # mask DMA loads per wave per tile
+    g["K_OFF"] = r; r += NKL
+    g["V_OFF"] = r; r += NKL
+    g["M_OFF"] = r; r += NML
+    g["K_RD"] = r; r += 8
+    g["V_RD"] = r; r += 4
+    g["M_RD"] = r; r += 4
+    g["MRUN"] = r; r += nh               # running max (u units) per half
+    g["MLOG"] = r; r += nh               # running max · c2
+    g["LSUM"] = r; r += nh               # this lane's partial row sums
+    # temporaries: widen temp, 16·g, per half: row max, swap temp, threshold;
+    # then alpha and a second widen temp
+    g["T"] = r; r += 4 + 3 * nh
+    g["FIN"] = r; r += 4                 # inputs: c2, 1/scale, slack, -inf
+    g["NEGINF"] = FIN + 3                # -inf in a VGPR (v_cndmask reads one of SGPR/VCC)
+    g["NVGPR"] = r
+    g["QA"] = 0                          # a[0 : 32·nh]   Q
+    g["OA"] = 32 * nh                    # a[32·nh : 96·nh] O
+    g["NAGPR"] = 96 * nh
+    g["WT0"], g["W16G"] = T + 0, T + 1
+    g["TMX"], g["TSW"], g["TTH"] = T + 2, T + 2 + nh, T + 2 + 2 * nh   # + h
+    g["TAL"], g["WT1"] = T + 2 + 3 * nh, T + 3 + 3 * nh
+    # bf16 mask chunks in flight: the mask window plus (idle during PV) K window
+    g["MSLOTS"] = [MWIN, MWIN + 4, KWIN, KWIN + 4, KWIN + 8, KWIN + 12][:6 if nh == 2 else 4]
+    g["NSLOT"] = len(MSLOTS)
+
+
+def S(p, h, b, i):
+    """Score register: buffer p, half h, 32-key block b, element i."""
+    return 2 * 0 + SBUF * p + 32 * h + 16 * b + i
+
+
+# required wait states (instructions issued) between producer and consumer,
+# as LLVM's hazard recognizer inserts them for gfx950, plus one of margin
+W_MFMA_VALU = 13      # 32x32x16 MFMA result -> VALU read/write
+W_VALU_MFMA = 3       # VALU write -> MFMA source
+W_MFMA_CHAIN = 3      # MFMA result -> the next MFMA accumulating into it
+W_TRANS = 2           # v_exp result -> VALU read
+W_VCC = 3             # VALU write of VCC -> lane-mask read
+W_PERM = 3            # VALU write -> v_permlane32_swap source
+
+
+class Stream:
+    """An instruction list with the wave's issue position and per-VGPR hazard
+    bookkeeping: ``need(regs, kind)`` pads with s_nop until the producer of each
+    register is far enough back."""
+
+    def __init__(self):
+        self.lines = []
+        self.pos = 0
+        self.ready = {}     # reg -> (position it was written, min distance for VALU readers)
+
+    def emit(self, text, n=1):
+        self.lines.append(text)
+        self.pos += n
+
+    def nop(self, k):
+        while k > 0:
+            c = min(k, 8)
+            self.emit(f"s_nop {c - 1}", c)
+            k -= c
+
+    def wait_for(self, regs, dist_key):
+        need = 0
+        for r in regs:
+            if r in self.ready:
+                at, d = self.ready[r]
+                dd = d.get(dist_key, 0)
+                need = max(need, at + dd - self.pos)
+        self.nop(need)
+
+    def wrote(self, regs, **dists):
+        for r in regs:
+            self.ready[r] = (self.pos, dists)
+
+
+def vrange(lo, n):
+    return list(range(lo, lo + n))
+
+
+def vreg(r, n=1):
+    return f"v{r}" if n == 1 else f"v[{r}:{r + n - 1}]"
+
+
+def areg(r, n=1):
+    return f"a{r}" if n == 1 else f"a[{r}:{r + n - 1}]"
+
+
+class Load:
+    """One LDS read: its text, destination registers and window slot. A slot is
+    reused only after every consumer of the previous load in it has issued."""
+
+    def __init__(self, text, dst, slot=None):
+        # the slot is the destination's first register: loads into the same
+        # registers (whichever window they belong to) are ordered by it
+        self.text, self.dst, self.slot = text, dst, dst[0]
+        self.consumers = 0
+        self.used = 0
+        self.index = None       # position in the issue order
+
+
+class Phase:
+    """Interleave MFMA items with VALU items (and scalar/DMA groups) into one
+    stream: after every MFMA, its share of VALU work. All LDS reads of the
+    phase issue in first-use order through one queue (at most MAXQ in flight,
+    slots recycled); before an instruction that needs a read, s_waitcnt
+    lgkmcnt(k) with k = reads issued after it (LDS reads complete in order).
+
+    item = dict(text=..., needs=[Load], src=[regs read], dst=[regs written],
+                kind='mfma'|'valu'|'trans'|'perm'|'vcc_write'|'vcc_read'|'raw'|'other')
+    """
+    MAXQ = 12
+
+    def __init__(self, st):
+        self.st = st
+
+    def run(self, mfmas, valus, others=(), valu_lead=0):
+        st = self.st
+        if "nolds" in ABL:
+            mfmas = [dict(m, needs=[]) for m in mfmas]
+            valus = [dict(v, needs=[]) for v in valus]
+        prog = []
+        valus, others = list(valus), list(others)
+        nm = len(mfmas)
+        per = (len(valus) - valu_lead + nm - 1) // nm if nm else 0
+        oper = (len(others) + nm - 1) // nm if nm else 0
+        oi = 0
+        vi = 0
+
+        def take_valu(limit_idx, mi):
+            # VALU items leave in list order; an item with min_mfma > mi waits
+            nonlocal vi
+            while vi < limit_idx and valus[vi].get("min_mfma", -1) <= mi:
+                prog.append(valus[vi])
+                vi += 1
+
+        take_valu(valu_lead, -1)
+        for mi, m in enumerate(mfmas):
+            deps = m.get("deps", ())
+            if deps:   # every VALU item tagged with one of deps goes before this MFMA
+                last = max((j for j in range(len(valus)) if valus[j].get("tag") in deps), default=-1)
+                take_valu(last + 1, mi - 1)
+                assert vi > last, "an MFMA's VALU dependency is held back by min_mfma"
+            prog.append(m)
+            mine = others[oi:oi + oper]    # one before this slot's VALU share, the rest after
+            oi += oper
+            prog += mine[:1]
+            take_valu(min(len(valus), vi + per), mi)
+            prog += mine[1:]
+        take_valu(len(valus), nm)
+        prog += valus[vi:] + others[oi:]
+        # loads in first-use order
+        order, seen = [], set()
+        for it in prog:
+            for ld in it.get("needs", []):
+                ld.consumers += 1
+                if id(ld) not in seen:
+                    seen.add(id(ld))
+                    order.append(ld)
+        last_in_slot = {}
+        prev = {}
+        for ld in order:
+            prev[id(ld)] = last_in_slot.get(ld.slot)
+            last_in_slot[ld.slot] = ld
+        issued = 0
+        complete = -1           # loads [0..complete] known landed
+
+        def try_issue():
+            nonlocal issued
+            while issued < len(order) and issued - 1 - complete < self.MAXQ:
+                ld = order[issued]
+                pv = prev[id(ld)]
+                if pv is not None and pv.used < pv.consumers:
+                    return
+                ld.index = issued
+                st.emit(ld.text)
+                issued += 1
+
+        for it in prog:
+            try_issue()
+            needs = it.get("needs", [])
+            if needs:
+                last = max(ld.index if ld.index is not None else 10 ** 9 for ld in needs)
+                assert last < 10 ** 9, "a needed LDS read could not be issued (slot deadlock)"
+                if last > complete:
+                    st.emit(f"s_waitcnt lgkmcnt({issued - 1 - last})")
+                    complete = last
+            emit_item(st, it)
+            for ld in needs:
+                ld.used += 1
+        try_issue()
+        assert issued == len(order)
+
+
+def emit_item(st, v):
+    kind = v.get("kind", "valu")
+    if kind == "dma":                 # SALU write of M0 -> LDS DMA: one wait state
+        if st.lines and st.lines[-1].startswith("s_add_u32 m0"):
+            st.emit("s_nop 0")
+    if kind in ("other", "m0", "dma"):
+        for line, n in v["lines"]:
+            st.emit(line, n)
+        return
+    if kind == "raw":
+        for line in v["lines"]:
+            st.emit(line)
+        return
+    reads = v.get("src", [])
+    if kind == "mfma":
+        st.wait_for(reads, "mfma")
+        st.emit(v["text"])
+        st.wrote(v.get("dst", []), valu=W_MFMA_VALU, mfma=W_MFMA_CHAIN)
+        return
+    if kind == "vcc_read":
+        st.wait_for(["vcc"], "vcc")
+    if kind == "perm":
+        st.wait_for(reads, "perm")
+    st.wait_for(reads, "valu")
+    st.emit(v["text"])
+    w = v.get("dst", [])
+    if kind == "trans":
+        st.wrote(w, valu=W_TRANS, mfma=W_VALU_MFMA, perm=W_PERM)
+    elif kind == "vcc_write":
+        st.wrote(["vcc"], vcc=W_VCC)
+    else:
+        st.wrote(w, valu=0, mfma=W_VALU_MFMA, perm=W_PERM)
+
+
+def interleave(a, b):
+    """Merge two ordered lists, alternating by their relative lengths."""
+    out, i, j = [], 0, 0
+    while i < len(a) or j < len(b):
+        if j >= len(b) or (i < len(a) and i * len(b) <= j * len(a)):
+            out.append(a[i]); i += 1
+        else:
+            out.append(b[j]); j += 1
+    return out
+
+
+def valu(text, reads=(), writes=(), kind="valu", needs=()):
+    return {"text": text, "src": list(reads), "dst": list(writes), "kind": kind,
+            "needs": list(needs)}
+
+
+def other(group):
+    return {"kind": "other", "lines": group}
+
+
+# ── instruction groups ───────────────────────────────────────────────────────
+def mfma_op(bf16):
+    return "v_mfma_f32_32x32x16_bf16" if bf16 else "v_mfma_f32_32x32x16_f16"
+
+
+def qk_mfmas(bf16, kstage_off, s_next):
+    """32 MFMAs of S_next = K·Qᵀ for both halves; each K operand (kd, kb) is
+    read once and feeds both halves. Chains S_next[h][kb] start from 0."""
+    out = []
+    slot = 0
+    for kd in range(KD):
+        for kb in range(2):
+            w = KWIN + 4 * (slot % 4)
+            off = kstage_off + kb * 32 * D * 2
+            ld = Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(K_RD + kd)} offset:{off}", vrange(w, 4),
+                      ("k", slot % 4))
+            slot += 1
+            for h in range(NH):
+                dst = S(s_next, h, kb, 0)
+                src_c = "0" if kd == 0 else vreg(dst, 16)
+                out.append({"kind": "mfma", "needs": [ld],
+                            "text": f"{mfma_op(bf16)} {vreg(dst, 16)}, {vreg(w, 4)}, "
+                                    f"{areg(QA + 32 * h + 4 * kd, 4)}, {src_c}",
+                            "dst": vrange(dst, 16),
+                            "src": vrange(w, 4) + (vrange(dst, 16) if kd else [])})
+    return out
+
+
+def pv_mfmas(bf16, vstage_off, s_cur):
+    """32 MFMAs of Oᵀ += Vᵀ·Pᵀ for both halves; each transposed V operand
+    (key step j, d block db) is read once (two 8-byte transposing reads)."""
+    out = []
+    slot = 0
+    for j in range(4):
+        for db in range(DB):
+            w = VWIN + 4 * (slot % 4)
+            off = vstage_off + ((j // 2) * 32 + (j % 2) * 8) * D * 2
+            l0 = Load(f"ds_read_b64_tr_b16 {vreg(w, 2)}, {vreg(V_RD + db)} offset:{off}",
+                      vrange(w, 2), ("v", slot % 4, 0))
+            l1 = Load(f"ds_read_b64_tr_b16 {vreg(w + 2, 2)}, {vreg(V_RD + db)} offset:{off + 4 * D * 2}",
+                      vrange(w + 2, 2), ("v", slot % 4, 1))
+            slot += 1
+            for h in range(NH):
+                pr = S(s_cur, h, 0, 0) + 4 * j      # P of key step j (bf16/fp16 pairs)
+                o = OA + 64 * h + 16 * db
+                out.append({"kind": "mfma", "needs": [l0, l1], "deps": (f"cvt{j}",),
+                            "text": f"{mfma_op(bf16)} {areg(o, 16)}, {vreg(w, 4)}, {vreg(pr, 4)}, "
+                                    f"{areg(o, 16)}",
+                            "dst": [], "src": vrange(w, 4) + vrange(pr, 4)})
+    return out
+
+
+def exp_only_valus(s_cur):
+    """exp2(u·c2 - m·c2) in place, fp32 (converted to P in Y by cvt_valus)."""
+    out = []
+    for grp in range(4):
+        for h in range(NH):
+            base = S(s_cur, h, 0, 0)
+            regs = [base + 8 * grp + e for e in range(8)]
+            for r in regs:
+                out.append(valu(f"v_fma_f32 v{r}, v{r}, %[c2], -v{MLOG + h}", [r, MLOG + h], [r]))
+            for r in regs:
+                out.append(valu(f"v_exp_f32 v{r}, v{r}", [r], [r], kind="trans"))
+    return out
+
+
+def cvt_valus(bf16, s_cur):
+    """Round the exponentials to P pairs in place; key step j of half h lands in
+    S(s_cur, h, 0, 0) + 4j .. +3 (tagged cvt{j} for the PV MFMAs of step j)."""
+    cvt = "v_cvt_pk_bf16_f32" if bf16 else "v_cvt_pk_f16_f32"
+    out = []
+    for grp in range(4):
+        for h in range(NH):
+            base = S(s_cur, h, 0, 0)
+            for k in range(4):
+                a, b = base + 8 * grp + 2 * k, base + 8 * grp + 2 * k + 1
+                dst = base + 4 * grp + k
+                it = valu(f"{cvt} v{dst}, v{a}, v{b}", [a, b], [dst])
+                it["tag"] = f"cvt{grp}"
+                out.append(it)
+    return out
+
+
+def exp_valus(bf16, s_cur):
+    """P = exp2(u·c2 - m·c2) rounded to the element type, in place: the P pairs
+    of key step j of half h land in S(s_cur, h, 0, 0) + 4j .. +3."""
+    cvt = "v_cvt_pk_bf16_f32" if bf16 else "v_cvt_pk_f16_f32"
+    out = []
+    for grp in range(4):                          # one P operand (8 scores) per half
+        for h in range(NH):
+            base = S(s_cur, h, 0, 0)
+            regs = [base + 8 * grp + e for e in range(8)]
+            for r in regs:
+                out.append(valu(f"v_fma_f32 v{r}, v{r}, %[c2], -v{MLOG + h}", [r, MLOG + h], [r]))
+            for r in regs:
+                out.append(valu(f"v_exp_f32 v{r}, v{r}", [r], [r], kind="trans"))
+            for k in range(4):
+                a, b = regs[2 * k], regs[2 * k + 1]
+                dst = base + 4 * grp + k
+                out.append(valu(f"{cvt} v{dst}, v{a}, v{b}", [a, b], [dst]))
+    return out
+
+
+def rowsum_valus(bf16, s_cur):
+    one = "0x3f803f80" if bf16 else "0x3c003c00"
+    op = "v_dot2c_f32_bf16" if bf16 else "v_dot2c_f32_f16"
+    out = []
+    for k in range(16):
+        for h in range(NH):
+            base = S(s_cur, h, 0, 0)
+            out.append(valu(f"{op} v{LSUM + h}, {one}, v{base + k}", [base + k, LSUM + h], [LSUM + h]))
+    return out
+
+
+def mask_add_valus(bf16, s_next, mstage_off):
+    """u += mask·(1/scale) for the next tile, both halves. The 16 mask values of
+    (half h, block b) are two 16-byte LDS reads into a window slot of 8."""
+    out = []
+    for idx, (h, b) in enumerate([(h, b) for h in range(NH) for b in range(2)]):
+        w = MWIN + 8 * (idx % 2)
+        off = mstage_off + h * 4096
+        lds = [Load(f"ds_read_b128 {vreg(w + 4 * i, 4)}, {vreg(M_RD + 2 * b + i)} offset:{off}",
+                    vrange(w + 4 * i, 4), ("m", idx % 2, i)) for i in range(2)]
+        for i in range(2):
+            for wd in range(4):
+                src = w + 4 * i + wd
+                lo = S(s_next, h, b, 8 * i + 2 * wd)
+                hi = lo + 1
+                nd = [lds[i]]
+                if bf16:
+                    out.append(valu(f"v_lshlrev_b32 v{WT0}, 16, v{src}", [src], [WT0], needs=nd))
+                    out.append(valu(f"v_and_b32 v{WT1}, 0xffff0000, v{src}", [src], [WT1], needs=nd))
+                    out.append(valu(f"v_fma_f32 v{lo}, v{WT0}, %[inv_scale], v{lo}", [WT0, lo], [lo]))
+                    out.append(valu(f"v_fma_f32 v{hi}, v{WT1}, %[inv_scale], v{hi}", [WT1, hi], [hi]))
+                else:
+                    out.append(valu(f"v_fma_mix_f32 v{lo}, v{src}, %[inv_scale], v{lo} op_sel_hi:[1,0,0]",
+                                    [src, lo], [lo], needs=nd))
+                    out.append(valu(f"v_fma_mix_f32 v{hi}, v{src}, %[inv_scale], v{hi} op_sel:[1,0,0] "
+                                    f"op_sel_hi:[1,0,0]", [src, hi], [hi], needs=nd))
+    return out
+
+
+def mask_mfma_items(s_next, mstage_off):
+    """bf16: u += mask·(1/scale) on the matrix core. The mask chunk of 16 keys
+    (half h, block b, chunk c: keys 32b + 16c + 8g .. +7 of this lane's row) is
+    the B operand as it sits in LDS; the A operand A_c (v[MSEL + 4c ..]) holds
+    bf16(1/scale) where its row's key (π-permuted, as in the score tile) is key
+    16c + k of its k index, else 0, so the MFMA adds mask·(1/scale) to exactly
+    the matching score. -inf is first clamped to -max_bf16 (v_pk_min_u16; 0 ×
+    -inf would be NaN); -max·(1/scale) overflows fp32 back to -inf because
+    bf16(1/scale) > 1.0078 (checked on the host). Returns (mfmas, valus)."""
+    mf, va = [], []
+    slots = MSLOTS
+    for idx, (h, b, c) in enumerate([(h, b, c) for h in range(NH) for b in range(2) for c in range(2)]):
+        w = slots[idx % len(slots)]
+        off = mstage_off + h * 4096
+        ld = Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(M_RD + 2 * b + c)} offset:{off}", vrange(w, 4),
+                  ("mm", idx % len(slots)))
+        tag = f"clamp{idx}"
+        for r in range(4):
+            it = valu(f"v_pk_min_u16 v{w + r}, v{w + r}, %[mclamp]", [w + r], [w + r], needs=[ld])
+            it["tag"] = tag
+            va.append(it)
+        dst = S(s_next, h, b, 0)
+        mf.append({"kind": "mfma", "needs": [ld], "deps": (tag,),   # the slot stays held until here
+                   "text": f"v_mfma_f32_32x32x16_bf16 {vreg(dst, 16)}, {vreg(MSEL + 4 * c, 4)}, "
+                           f"{vreg(w, 4)}, {vreg(dst, 16)}",
+                   "dst": vrange(dst, 16), "src": vrange(w, 4) + vrange(dst, 16)})
+    return mf, va
+
+
+def tail_item(label, s_next, left=1):
+    """Keys at or past Sk in the tile being scored -> -inf. Taken only when that
+    tile is the last one (s92 == 1) and Sk % 64 != 0 (%[lim] = valid keys < 64).
+    Lane (row, half g) owns keys 32b + 16g + i of block b."""
+    lines = [f"s_cmp_eq_u32 s92, {left}", f"s_cbranch_scc0 {label}_skip",
+             "s_cmp_eq_u32 %[lim], 64", f"s_cbranch_scc1 {label}_skip",
+             f"v_sub_u32 v{WT1}, %[lim], v{W16G}"]
+    for b in range(2):
+        for i in range(16):
+            lines += [f"v_cmp_lt_i32 vcc, {32 * b + i}, v{WT1}", "s_nop 2"]
+            for h in range(NH):
+                r = S(s_next, h, b, i)
+                lines.append(f"v_cndmask_b32 v{r}, v{NEGINF}, v{r}, vcc")
+    lines += ["s_nop 1", f"{label}_skip:"]
+    return {"kind": "raw", "lines": lines}
+
+
+def max_valus(s_next):
+    """Row max of the next tile per half into v(TMX+h) (both 32-lane halves of
+    a row combined), then the rescale test: lanes whose max exceeds the running
+    max by more than the slack set their bit in s[94:95]."""
+    out = []
+    for h in range(NH):
+        mx = TMX + h
+        regs = [S(s_next, h, b, i) for b in range(2) for i in range(16)]
+        out.append(valu(f"v_max3_f32 v{mx}, v{regs[0]}, v{regs[1]}, v{regs[2]}", regs[:3], [mx]))
+        k = 3
+        while k < 32:
+            pair = regs[k:k + 2]
+            if len(pair) == 2:
+                out.append(valu(f"v_max3_f32 v{mx}, v{mx}, v{pair[0]}, v{pair[1]}", [mx] + pair, [mx]))
+            else:
+                out.append(valu(f"v_max_f32 v{mx}, v{mx}, v{pair[0]}", [mx] + pair, [mx]))
+            k += 2
+    for h in range(NH):
+        mx, tmp = TMX + h, TSW + h
+        out.append(valu(f"v_mov_b32 v{tmp}, v{mx}", [mx], [tmp]))
+        out.append(valu(f"v_permlane32_swap_b32 v{mx}, v{tmp}", [mx, tmp], [mx, tmp], kind="perm"))
+    for h in range(NH):
+        mx, tmp, th = TMX + h, TSW + h, TTH + h
+        out.append(valu(f"v_max_f32 v{mx}, v{mx}, v{tmp}", [mx, tmp], [mx]))
+        out.append(valu(f"v_add_f32 v{th}, %[slack], v{MRUN + h}", [MRUN + h], [th]))
+    for h in range(NH):
+        mx, th = TMX + h, TTH + h
+        out.append(valu(f"v_cmp_gt_f32 vcc, v{mx}, v{th}", [mx, th], [], kind="vcc_write"))
+        out.append({"kind": "raw", "lines": [
+            "s_nop 2", "s_mov_b64 s[94:95], vcc" if h == 0 else "s_or_b64 s[94:95], s[94:95], vcc"]})
+    return out
+
+
+def rescale_lines(label):
+    """Taken when some row's max grew past the slack (rare): per lane alpha =
+    exp2((m_old - m_new)·c2) (1 for lanes keeping their max), O and l scaled,
+    running max and max·c2 updated. Waits for every PV MFMA first."""
+    lines = ["s_cmp_eq_u64 s[94:95], 0", f"s_cbranch_scc1 {label}_skip", "s_nop 7", "s_nop 7"]
+    al, tmp = TAL, WT1
+    for h in range(NH):
+        mx, th = TMX + h, TTH + h
+        lines += [
+            f"v_cmp_gt_f32 vcc, v{mx}, v{th}",
+            f"v_sub_f32 v{al}, v{MRUN + h}, v{mx}",
+            f"v_mul_f32 v{al}, %[c2], v{al}",
+            f"v_exp_f32 v{al}, v{al}",
+            "s_nop 2",
+            f"v_cndmask_b32 v{al}, 1.0, v{al}, vcc",
+            f"v_cndmask_b32 v{MRUN + h}, v{MRUN + h}, v{mx}, vcc",
+            f"v_mul_f32 v{LSUM + h}, v{LSUM + h}, v{al}",
+            f"v_mul_f32 v{MLOG + h}, %[c2], v{MRUN + h}",
+            f"v_cmp_eq_f32 vcc, %[neginf], v{MRUN + h}",
+            "s_nop 2",
+            f"v_cndmask_b32_e64 v{MLOG + h}, v{MLOG + h}, 0, vcc",
+        ]
+        for r in range(64):
+            a = OA + 64 * h + r
+            lines += [f"v_accvgpr_read_b32 v{tmp}, a{a}", "s_nop 1",
+                      f"v_mul_f32 v{tmp}, v{tmp}, v{al}", "s_nop 1",
+                      f"v_accvgpr_write_b32 a{a}, v{tmp}"]
+    lines += ["s_nop 7", f"{label}_skip:"]
+    return lines
+
+
+def dma_items(stage_k, stage_v, stage_m, do_k, do_v, do_m):
+    """LDS DMA of one tile as single-instruction items: per 16-byte-per-lane
+    load, the M0 write (LDS destination: lane i lands at M0 + 16·i) and then the
+    load, kept at least one instruction apart by emit_item. Each descriptor then
+    moves on by one tile: base up, remaining size down, saturating at 0, so a
+    load for a tile past the end is out of range (reads nothing, writes no LDS)."""
+    items = []
+
+    def one(sl, lds, off, v):
+        items.append({"kind": "m0", "lines": [(f"s_add_u32 m0, %[{lds}], {off}", 1)]})
+        items.append({"kind": "dma", "lines": [(f"buffer_load_dwordx4 v{v}, s[{sl}:{sl + 3}], 0 offen lds", 1)]})
+
+    def adv(sl, step):
+        items.append({"kind": "other", "lines": [
+            (f"s_add_u32 s{sl}, s{sl}, {step}", 1), (f"s_addc_u32 s{sl + 1}, s{sl + 1}, 0", 1),
+            (f"s_sub_u32 s{sl + 2}, s{sl + 2}, {step}", 1), (f"s_cselect_b32 s{sl + 2}, 0, s{sl + 2}", 1)]})
+    if do_k:
+        for i in range(NKL):
+            one(80, "lds_k", stage_k * KSTAGE + i * WAVES * 1024, K_OFF + i)
+        adv(80, "%[kstep]")
+    if do_v:
+        for i in range(NKL):
+            one(84, "lds_v", stage_v * KSTAGE + i * WAVES * 1024, V_OFF + i)
+        adv(84, "%[vstep]")
+    if do_m:
+        for i in range(NML):
+            one(88, "lds_m", stage_m * MSTAGE + i * 1024, M_OFF + i)
+        adv(88, "128")
+    return items
+
+
+def emit_groups(st, items):
+    for it in items:
+        emit_item(st, it)
+
+
+def gen(bf16: bool, nh: int = 2) -> str:
+    configure(nh)
+    st = Stream()
+    L = f"fa_w{32 * NH}_%="
+    # entry: Q -> AGPRs, O = 0, running state, 16·g of this lane
+    for r in range(32 * NH):
+        st.emit(f"v_accvgpr_write_b32 a{QA + r}, v{r}")
+    for r in range(64 * NH):
+        st.emit(f"v_accvgpr_write_b32 a{OA + r}, 0")
+    for h in range(NH):
+        st.emit(f"v_mov_b32 v{MRUN + h}, %[neginf]")
+        st.emit(f"v_mov_b32 v{MLOG + h}, 0")
+        st.emit(f"v_mov_b32 v{LSUM + h}, 0")
+    st.emit(f"v_mbcnt_lo_u32_b32 v{W16G}, -1, 0")
+    st.emit(f"v_mbcnt_hi_u32_b32 v{W16G}, -1, v{W16G}")
+    st.emit(f"v_lshrrev_b32 v{W16G}, 5, v{W16G}")
+    st.emit(f"v_lshlrev_b32 v{W16G}, 4, v{W16G}")
+    for base, names in ((80, ("klo", "khi", "kn", "fl")), (84, ("vlo", "vhi", "vn", "fl")),
+                        (88, ("mlo", "mhi", "mn", "fl"))):
+        for i, nm in enumerate(names):
+            st.emit(f"s_mov_b32 s{base + i}, %[{nm}]")
+    st.emit("s_mov_b32 s92, %[ntiles]")          # tiles left to score, including the next one
+    if "ts" in ABL:
+        st.emit("s_mov_b64 s[96:97], %[dbgp]")
+    st.nop(4)
+    st.ready.clear()
+
+    # prologue: tile nb's K, mask, V into stage 0; nb+1's K and mask into stage 1
+    emit_groups(st, dma_items(0, 0, 0, True, True, True))
+    emit_groups(st, dma_items(1, 0, 1, True, False, True))
+    st.emit("s_waitcnt vmcnt(0)")
+    st.emit("s_barrier")
+    Phase(st).run(qk_mfmas(bf16, K_LDS, 0), [])
+    if bf16:
+        mm, clamps = mask_mfma_items(0, M_LDS)
+        Phase(st).run(mm, clamps)
+        st.nop(W_MFMA_VALU)
+        Phase(st).run([], [tail_item(f"{L}_t0", 0)] + max_valus(0))
+    else:
+        Phase(st).run([], mask_add_valus(bf16, 0, M_LDS) + [tail_item(f"{L}_t0", 0)] + max_valus(0))
+    for line in rescale_lines(f"{L}_r0"):
+        st.emit(line)
+    st.ready.clear()
+
+    def stamp(k):
+        if "ts" not in ABL:
+            return
+        # the V window is idle at every stamp point; the pointer lives in s[96:97]
+        for line in ["s_memtime s[98:99]", "s_waitcnt lgkmcnt(0)", f"v_mov_b32 v{VWIN}, s98",
+                     f"v_mov_b32 v{VWIN + 1}, s99", f"v_mov_b32 v{VWIN + 2}, 0",
+                     f"global_store_dwordx2 v{VWIN + 2}, v[{VWIN}:{VWIN + 1}], s[96:97] offset:{8 * k}"]:
+            st.emit(line)
+        if k == 3:
+            st.emit("s_add_u32 s96, s96, 32")
+            st.emit("s_addc_u32 s97, s97, 0")
+
+    def body(p, last):
+        nxt = 1 - p
+        lab = f"{L}_b{p}{'L' if last else ''}"
+        if "nobar" not in ABL:
+            st.emit("s_waitcnt vmcnt(0) lgkmcnt(0)")
+            st.emit("s_barrier")
+        else:
+            st.emit("s_waitcnt lgkmcnt(0)")
+        stamp(0)
+        if last:
+            Phase(st).run([], exp_only_valus(p))
+            Phase(st).run(pv_mfmas(bf16, V_LDS + p * KSTAGE, p), cvt_valus(bf16, p) + rowsum_valus(bf16, p))
+            return
+        # tile n+2's K and mask into stage p (out of range past the last tile),
+        # tile n+1's V into stage 1-p: single instructions spread over the tile
+        others = [] if "nodma" in ABL else dma_items(p, nxt, p, True, True, "nodmam" not in ABL)
+        # One stream per tile: QK(n+1) then PV(n) (with the bf16 mask MFMAs of
+        # n+1 between the first PV MFMAs) on the matrix core; exp(n), cvt(n),
+        # clamps, row sums, tail and max of n+1 on the VALU. One load queue,
+        # so V and mask reads of PV prefetch under the end of QK.
+        qk = [] if "noqk" in ABL else qk_mfmas(bf16, K_LDS + nxt * KSTAGE, nxt)
+        pv = [] if "nopv" in ABL else pv_mfmas(bf16, V_LDS + p * KSTAGE, p)
+        ex = [] if "noexp" in ABL else exp_only_valus(p)
+        if bf16:
+            mm, clamps = mask_mfma_items(nxt, M_LDS + nxt * MSTAGE)
+            mfy = []
+            for i, m in enumerate(pv):
+                mfy.append(m)
+                if i % 2 == 1 and mm:
+                    mfy.append(mm.pop(0))
+            mfy += mm
+            mf = qk + mfy
+            mpos = [i for i, m in enumerate(mf) if "clamp" in m.get("deps", ("",))[0]]
+            # chunk k shares its window slot with chunk k-NSLOT
+            for it in clamps:
+                k = int(it["tag"][5:])
+                if k >= NSLOT:
+                    it["min_mfma"] = mpos[k - NSLOT]
+            late = [tail_item(f"{lab}_t", nxt, left=2)] + max_valus(nxt)
+            for it in late:
+                it["min_mfma"] = mpos[-1]
+            vy = interleave(cvt_valus(bf16, p), clamps) + rowsum_valus(bf16, p) + late
+        else:
+            mf = qk + pv
+            late = mask_add_valus(bf16, nxt, M_LDS + nxt * MSTAGE) + \
+                [tail_item(f"{lab}_t", nxt, left=2)] + max_valus(nxt)
+            for it in late:     # they read the QK results: after the last QK MFMA
+                it["min_mfma"] = len(qk) - 1
+            vy = cvt_valus(bf16, p) + rowsum_valus(bf16, p) + late
+        if "novaluy" in ABL:
+            vy = [{"kind": "raw", "lines": ["s_mov_b64 s[94:95], 0"]}]
+        Phase(st).run(mf, ex + vy, others, valu_lead=0 if "noexp" in ABL else 8)
+        st.emit("s_sub_u32 s92, s92, 1")
+        stamp(1)
+        stamp(2)
+        for line in rescale_lines(f"{lab}_r"):
+            st.emit(line)
+        stamp(3)
+        st.ready.clear()
+
+    st.emit(f"{L}_loop:")
+    st.emit("s_cmp_le_u32 s92, 1")
+    st.emit(f"s_cbranch_scc1 {L}_last0")
+    body(0, False)
+    st.emit("s_cmp_le_u32 s92, 1")
+    st.emit(f"s_cbranch_scc1 {L}_last1")
+    body(1, False)
+    st.emit(f"s_branch {L}_loop")
+    st.emit(f"{L}_last0:")
+    body(0, True)
+    st.emit(f"s_branch {L}_end")
+    st.emit(f"{L}_last1:")
+    body(1, True)
+    st.emit(f"{L}_end:")
+    # O out of the AGPRs once the last PV MFMA has finished
+    st.nop(16)
+    for r in range(64 * NH):
+        st.emit(f"v_accvgpr_read_b32 v{r}, a{OA + r}")
+    st.nop(2)
+    return "\n".join(st.lines)
+
+
+def operand_macros(prefix, bf16):
+    """The asm statement's operand lists for one kernel: outputs and inputs
+    bound to the physical registers the loop text uses, plus the clobbers."""
+    outs = [f'"={{{vreg(16 * i, 16)}}}"(o[{i}])' for i in range(4 * NH)]
+    outs += [f'"={{v{MRUN + h}}}"(mrun[{h}])' for h in range(NH)]
+    outs += [f'"={{v{LSUM + h}}}"(lsum[{h}])' for h in range(NH)]
+    ins = [f'"{{{vreg(32 * h, 32)}}}"(q[{h}])' for h in range(NH)]
+    ins += [f'"{{{vreg(K_OFF, NKL)}}}"(koff)', f'"{{{vreg(V_OFF, NKL)}}}"(voff)',
+            f'"{{{vreg(M_OFF, NML)}}}"(moff)', f'"{{{vreg(K_RD, 8)}}}"(krd)',
+            f'"{{{vreg(V_RD, 4)}}}"(vrd)', f'"{{{vreg(M_RD, 4)}}}"(mrd)']
+    if bf16:
+        ins += [f'"{{{vreg(MSEL, 8)}}}"(msel)', '[mclamp] "s"(mclamp)']
+    ins += [f'[c2] "{{v{FIN}}}"(c2)', f'[inv_scale] "{{v{FIN + 1}}}"(inv_scale)',
+            f'[slack] "{{v{FIN + 2}}}"(slack)', f'[neginf] "{{v{FIN + 3}}}"(neginf)']
+    ins += [f'[{n}] "s"({n})' for n in ("lim", "lds_k", "lds_v", "lds_m", "kstep", "vstep", "klo", "khi",
+                                         "kn", "vlo", "vhi", "vn", "mlo", "mhi", "mn", "fl", "ntiles")]
+    clob = list(range(KWIN, MWIN + 8)) + ([] if bf16 else list(range(MSEL, MSEL + 8)))
+    clob += [MLOG + h for h in range(NH)] + list(range(T, FIN))
+    cl = [f'"v{r}"' for r in clob] + [f'"a{r}"' for r in range(NAGPR)]
+    cl += [f'"s{r}"' for r in range(80, 98)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
+    if "ts" in ABL:     # timing-only scratch builds: the timestamp pointer (SGPR pair)
+        ins.append('[dbgp] "s"(dbgp)')
+        cl += ['"s98"', '"s99"']
+    dt = "BF16" if bf16 else "F16"
+    return [f"#define {prefix}_OUTPUTS_{dt} " + ", ".join(outs),
+            f"#define {prefix}_INPUTS_{dt} " + ", ".join(ins),
+            f"#define {prefix}_CLOBBERS_{dt} " + ", ".join(cl)]
+
+
+def render() -> str:
+    parts = ["// Generated by gen_fa_loop.py -- do not edit.",
+             "// Software-pipelined tile loops (gfx950 assembly) of the 32- and 64-rows-per-wave",
+             "// kernels, one string per element type, with the operand bindings they assume.",
+             "#pragma once"]
+    for nh, prefix in ((2, "MI355_W64"), (1, "MI355_W32")):
+        for bf16 in (True, False):
+            text = gen(bf16, nh)
+            dt = "BF16" if bf16 else "F16"
+            parts += operand_macros(prefix, bf16)
+            parts.append(f"#define {prefix}_LOOP_{dt} \\")
+            for line in text.split("\n"):
+                parts.append(f'  "{line}\\n\\t" \\')
+            parts.append('  ""')
+        parts.append(f"// {prefix}: {NVGPR} VGPRs and {NAGPR} AGPRs of the loop's own")
+    return "\n".join(parts) + "\n"
+
+
+if __name__ == "__main__":
+    txt = render()
+    if len(sys.argv) > 2 and sys.argv[1] == "--out":
+        with open(sys.argv[2], "w") as f:
+            f.write(txt)
+        sys.exit(0)
+    if len(sys.argv) > 1 and sys.argv[1] == "--check":
+        with open(OUT) as f:
+            sys.exit(0 if f.read() == txt else 1)
+    with open(OUT, "w") as f:
+        f.write(txt)
+    print(OUT, txt.count("\\n"), "lines")

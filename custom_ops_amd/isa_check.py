@@ -11,6 +11,7 @@ never produced, and by ``tests/test_isa.py``.
   the feature; this catches a flag that went missing.
 * No register spills and no scratch memory in any kernel (a kernel that fell
   back to scratch ran 16x slower while still passing every numeric test).
+* Every kernel's register need fits its workgroup size (waves per SIMD).
 """
 from __future__ import annotations
 
@@ -60,4 +61,17 @@ def violations(text: str) -> list:
             out.append(f"spills or scratch in {name}: {f}")
     if "scratch_" in "\n".join(code_outside_asm(text)):
         out.append("scratch instructions present")
+    # Register need must fit the launch bounds: a SIMD holds 512 registers per
+    # lane, shared by the waves of a workgroup that land on it (inline assembly
+    # bound to fixed registers can push a kernel past its budget without a
+    # compiler error).
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)\n(.*?)\.end_amdhsa_kernel", text, re.S):
+        nf = re.search(r"\.amdhsa_next_free_vgpr (\d+)", m.group(2))
+        meta = dict(kernel_metadata(text)).get(m.group(1), {})
+        wg = int(meta.get("max_flat_workgroup_size", 0) or 0)
+        if nf and wg:
+            per_simd = -(-wg // 256)
+            if int(nf.group(1)) > 512 // per_simd:
+                out.append(f"{m.group(1)} needs {nf.group(1)} registers per wave but its "
+                           f"{wg}-thread workgroup puts {per_simd} waves on a SIMD")
     return out
