@@ -157,6 +157,7 @@ struct KParams {
   int q_rs, k_rs, v_rs, o_rs, m_rs;  // row strides (elements)
 
   int b, h, ratio;   // ratio = H / Hk
+  int pack;          // q-heads per workgroup (they share one KV head), divides ratio
   int sq, sk;
   int msq;           // mask rows present
   int num_m;         // ceil(Sq / BM)
@@ -259,27 +260,42 @@ struct TileIdx {
   int b, h, hk, split, m0, nb, ne;
 };
 
+// A workgroup of BM query rows serves p.pack heads that share one KV head
+// (GQA), BM / p.pack rows of each: its K/V tiles serve every wave as before,
+// and the waves of different heads read the same mask rows at the same time.
+// tile_index gives the group's first head; place_wave moves one wave to its
+// head h + w % pack and row slot w / pack.
 template <int BM>
 __device__ __forceinline__ TileIdx tile_index(const KParams& p) {
   TileIdx ti;
   int t = xcd_remap(blockIdx.x, p.total);
-  int mb;
-  if (p.head_major) {   // (b, split, m-block, h): the heads sharing a mask tile run together
-    ti.h = t % p.h;  t /= p.h;
+  const int ng = p.h / p.pack;   // head groups per batch
+  int mb, hg;
+  if (p.head_major) {   // (b, split, m-block, head group): the heads sharing a mask tile run together
+    hg = t % ng;  t /= ng;
     mb = t % p.num_m;  t /= p.num_m;
     ti.split = t % p.num_splits;
     ti.b = t / p.num_splits;
-  } else {              // (b, h, split, m-block): the m-blocks sharing K/V run together
+  } else {              // (b, head group, split, m-block): the m-blocks sharing K/V run together
     mb = t % p.num_m;  t /= p.num_m;
     ti.split = t % p.num_splits;  t /= p.num_splits;
-    ti.h = t % p.h;
-    ti.b = t / p.h;
+    hg = t % ng;
+    ti.b = t / ng;
   }
+  ti.h = hg * p.pack;
   ti.hk = ti.h / p.ratio;
-  ti.m0 = mb * BM;
+  ti.m0 = mb * (BM / p.pack);
   ti.nb = ti.split * p.n_per_split;
   ti.ne = min(ti.nb + p.n_per_split, p.num_n);
   return ti;
+}
+
+// Wave w of a packed workgroup: head h + w % pack, rows from m0 + (w / pack)·rows.
+// m0 is rebased so that m0 + w·rows stays the wave's first row (every row
+// expression below is written that way; LDS slots stay indexed by w).
+__device__ __forceinline__ void place_wave(TileIdx& ti, const KParams& p, int wave, int rows) {
+  ti.h += wave % p.pack;
+  ti.m0 += (wave / p.pack - wave) * rows;
 }
 
 // ── main kernel: 32 query rows per wave, WAVES = 4 or 8 waves ─────────────────
@@ -737,7 +753,8 @@ void fa_fwd_kernel(const KParams p) {
   __shared__ __align__(16) uint16_t sV[NST][G::kVElems];
   __shared__ __align__(16) uint16_t sM[A::MREG ? 8 : G::kMElems];
 
-  const TileIdx ti = tile_index<G::kBM>(p);
+  TileIdx ti = tile_index<G::kBM>(p);
+  place_wave(ti, p, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), 32);
   A a(p);
   a.init(ti);
   const int nb = ti.nb, ne = ti.ne;
@@ -886,9 +903,10 @@ void fa_fwd_kernel_asm(const KParams p) {
   constexpr int NML = 4 * NH;                      // mask DMA loads per wave per tile
   constexpr int ROWS = 32 * NH;                    // query rows per wave
   __shared__ __align__(16) uint8_t smem[kAsmLds];
-  const TileIdx ti = tile_index<256>(p);
+  TileIdx ti = tile_index<256>(p);
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  place_wave(ti, p, wave, ROWS);
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
 
   const uint16_t* kbase = p.k + (int64_t)ti.b * p.k_bs + (int64_t)ti.hk * p.k_hs;
@@ -1188,6 +1206,7 @@ static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int 
 
 struct Plan {
   int waves, block_m, num_m, num_n, splits, n_per_split;
+  int pack;   // q-heads per workgroup; block_m / pack rows of each
   int head_major;
   size_t o_part_bytes, lse_bytes, ws_bytes;
 };
@@ -1211,8 +1230,8 @@ constexpr PlanCost kCostD128 = {1.819f, 3.630f, 2.197f, 1.258f, 1.923f, 5.251f, 
 constexpr PlanCost kCostD64 = {1.334f, 2.139f, 1.427f, 0.932f, 1.109f, 5.791f, 0.417f, 0.128f};
 
 static float plan_cost(const PlanCost& c, int bh, int sq, int num_n, int d, int waves, int s,
-                       int cus) {
-  const int64_t wgs = (int64_t)bh * ceil_div(sq, 32 * waves) * s;
+                       int cus, int pack = 1) {
+  const int64_t wgs = (int64_t)(bh / pack) * ceil_div(sq, 32 * waves / pack) * s;
   const int64_t k = (wgs + cus - 1) / cus;   // workgroups on the busiest CU
   const float nps = (float)ceil_div(num_n, s);
   float t = waves == 8 ? (float)k * (nps * c.t8 + c.o8)
@@ -1221,8 +1240,23 @@ static float plan_cost(const PlanCost& c, int bh, int sq, int num_n, int d, int 
   return t;
 }
 
+// Heads per workgroup: GQA heads that share a KV head also share the mask
+// rows, so packing them makes the waves of one workgroup read the same mask
+// rows together. A power of two dividing H / Hk, at most 4 (the 4-wave
+// workgroups and the 64-row waves of the 4-wave assembly form hold 4 heads).
+static int pick_pack(const mi355_fa_params* p) {
+  const int ratio = p->h / p->h_k;
+  int want = 4;
+  const char* e = getenv("MI355_FA_PACK");   // tuning override: 1, 2 or 4
+  if (e && (atoi(e) == 1 || atoi(e) == 2 || atoi(e) == 4)) want = atoi(e);
+  int pk = 1;
+  while (pk * 2 <= want && ratio % (pk * 2) == 0) pk *= 2;
+  return pk;
+}
+
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
+  pl.pack = pick_pack(p);
   pl.num_n = ceil_div(p->seqlen_k, kBN);
   const int bh = p->b * p->h;
   int s_fixed = p->num_splits;
@@ -1245,7 +1279,7 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   for (int w = 4; w <= 8; w += 4) {
     if (w_fixed && w != w_fixed) continue;
     for (int s = s_fixed > 0 ? s_fixed : 1; s <= (s_fixed > 0 ? s_fixed : max_s); ++s) {
-      const float c = plan_cost(cm, bh, p->seqlen_q, pl.num_n, p->d, w, s, cus);
+      const float c = plan_cost(cm, bh, p->seqlen_q, pl.num_n, p->d, w, s, cus, pl.pack);
       if (pl.waves == 0 || c < best) { best = c; pl.waves = w; pl.splits = s; }
     }
   }
@@ -1256,13 +1290,13 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   // own L2. With few m-blocks per head, the mask tile (shared by all heads of
   // a batch) is the stream worth sharing: heads fastest. Otherwise the K/V of
   // a head (shared by its m-blocks) is: m-blocks fastest.
-  pl.head_major = ceil_div(p->seqlen_q, pl.block_m) <= 2 ? 1 : 0;
+  pl.head_major = ceil_div(p->seqlen_q, pl.block_m / pl.pack) <= 2 ? 1 : 0;
   {
     const char* o = getenv("MI355_FA_ORDER");   // tuning override: "h" or "m"
     if (o && o[0] == 'h') pl.head_major = 1;
     if (o && o[0] == 'm') pl.head_major = 0;
   }
-  pl.num_m = ceil_div(p->seqlen_q, pl.block_m);
+  pl.num_m = ceil_div(p->seqlen_q, pl.block_m / pl.pack);
   pl.n_per_split = (s > 1) ? ceil_div(pl.num_n, s) : pl.num_n;
   if (s > 1) {
     const size_t rows = (size_t)s * p->b * p->h * p->seqlen_q;
@@ -1415,7 +1449,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
     return MI355_FA_EDEVICE;
   }
   const Plan pl = make_plan(p, dev.cus);
-  const int64_t total = (int64_t)p->b * p->h * pl.num_m * pl.splits;
+  const int64_t total = (int64_t)p->b * (p->h / pl.pack) * pl.num_m * pl.splits;
   if (total >= (1LL << 24)) {
     set_err(err, errlen, "problem too large: %lld workgroups", (long long)total);
     return MI355_FA_EINVAL;
@@ -1423,7 +1457,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   // Buffer offsets are 32-bit: every per-head / per-batch byte range the kernel
   // addresses (including the rounded-up last row tile) must stay below 2^32.
   {
-    const uint64_t rows_q = (uint64_t)pl.num_m * pl.block_m, rows_k = (uint64_t)pl.num_n * kBN;
+    const uint64_t rows_q = (uint64_t)pl.num_m * (pl.block_m / pl.pack), rows_k = (uint64_t)pl.num_n * kBN;
     const uint64_t lim = 0xffffffffull - 4096;
     const uint64_t need[] = {
         rows_q * (uint64_t)p->q_row_stride * 2, rows_q * (uint64_t)p->o_row_stride * 2,
@@ -1455,7 +1489,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.v_bs = p->v_batch_stride; kp.v_hs = p->v_head_stride; kp.v_rs = (int)p->v_row_stride;
   kp.o_bs = p->o_batch_stride; kp.o_hs = p->o_head_stride; kp.o_rs = (int)p->o_row_stride;
   kp.m_bs = p->mask_batch_stride; kp.m_rs = (int)p->mask_row_stride;
-  kp.b = p->b; kp.h = p->h; kp.ratio = p->h / p->h_k;
+  kp.b = p->b; kp.h = p->h; kp.ratio = p->h / p->h_k; kp.pack = pl.pack;
   kp.sq = p->seqlen_q; kp.sk = p->seqlen_k; kp.msq = p->mask_seqlen_q;
   kp.num_m = pl.num_m; kp.num_n = pl.num_n;
   kp.num_splits = pl.splits; kp.n_per_split = pl.n_per_split;

@@ -52,6 +52,7 @@ OUT = os.path.join(HERE, "fa_loop.inc")
 # timestamps into a debug buffer whose address the scratch build binds to
 # v[231:232])
 ABL = set(filter(None, os.environ.get("W64_ABLATE", "").split(",")))
+PRIO_STEPS = next((int(a[4:]) for a in ABL if a.startswith("prio")), 0)
 
 D = 128
 KD = D // 16          # 16-d steps of QK
@@ -671,6 +672,24 @@ def gen(bf16: bool, nh: int = 2) -> str:
             st.emit("s_add_u32 s96, s96, 32")
             st.emit("s_addc_u32 s97, s97, 0")
 
+    def prio_steps(start, nm):
+        # Two waves share each SIMD and the older one wins issue ties, so it
+        # finishes its tile early and idles at the barrier while the younger
+        # one runs alone. The priority drops as a wave gets through its
+        # MFMAs, so the wave that is behind gets the issue slots.
+        steps = PRIO_STEPS
+        if not steps:
+            return
+        marks = {round(nm * (k + 1) / steps): steps - 1 - k for k in range(steps - 1)}
+        out, seen = [], 0
+        for line in st.lines[start:]:
+            out.append(line)
+            if line.startswith("v_mfma"):
+                seen += 1
+                if seen in marks:
+                    out.append(f"s_setprio {marks[seen]}")
+        st.lines[start:] = out
+
     def body(p, last):
         nxt = 1 - p
         lab = f"{L}_b{p}{'L' if last else ''}"
@@ -679,6 +698,8 @@ def gen(bf16: bool, nh: int = 2) -> str:
             st.emit("s_barrier")
         else:
             st.emit("s_waitcnt lgkmcnt(0)")
+        if PRIO_STEPS:
+            st.emit(f"s_setprio {PRIO_STEPS - 1}")
         stamp(0)
         if last:
             Phase(st).run([], exp_only_valus(p))
@@ -722,7 +743,9 @@ def gen(bf16: bool, nh: int = 2) -> str:
             vy = cvt_valus(bf16, p) + rowsum_valus(bf16, p) + late
         if "novaluy" in ABL:
             vy = [{"kind": "raw", "lines": ["s_mov_b64 s[94:95], 0"]}]
+        start = len(st.lines)
         Phase(st).run(mf, ex + vy, others, valu_lead=0 if "noexp" in ABL else 8)
+        prio_steps(start, len(mf))
         st.emit("s_sub_u32 s92, s92, 1")
         stamp(1)
         stamp(2)
@@ -745,6 +768,8 @@ def gen(bf16: bool, nh: int = 2) -> str:
     st.emit(f"{L}_last1:")
     body(1, True)
     st.emit(f"{L}_end:")
+    if PRIO_STEPS:
+        st.emit("s_setprio 0")
     # O out of the AGPRs once the last PV MFMA has finished
     st.nop(16)
     for r in range(64 * NH):
