@@ -1055,6 +1055,7 @@ struct CParams {
   int64_t o_bs, o_hs, o_rs;
   int b, h, sq, num_splits;
   int64_t rows;  // B*H*Sq
+  uint32_t part_bytes;   // bytes of o_part when below 2^31 (buffer-addressed loads), else 0
 };
 
 // Workgroup = kCombineThreads / (D/8) rows × D columns: 256 threads (16 rows
@@ -1105,15 +1106,37 @@ __global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CPara
   if (row >= p.rows) return;
   const uint16_t* src = p.o_part + row * D + c8 * 8;
   f32x8 acc = {};
-  for (int s0 = 0; s0 < S; s0 += kBatch) {
-    u32x4 raw[kBatch];
+  // A split with weight 0 (lse = -inf: no live key of the row in that split,
+  // e.g. outside a sliding window) adds exactly nothing, so its partial is not
+  // fetched (cf. the active-split mask of csrc/fa/sm89/fa_fwd_kernel.h:1458-1468;
+  // here per row). Branch-free: the lane's buffer offset moves past the end
+  // of the partials, and an out-of-range buffer load returns 0 without a
+  // memory access, keeping every split's load of the batch in flight together.
+  if (p.part_bytes) {
+    const rsrc_t rp = make_rsrc(p.o_part, p.part_bytes);
+    const uint32_t off0 = (uint32_t)((row * D + c8 * 8) * 2);
+    const uint32_t sstep = (uint32_t)(slab * D * 2);
+    for (int s0 = 0; s0 < S; s0 += kBatch) {
+      u32x4 raw[kBatch];
+      float w[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (s0 + u < S) raw[u] = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + u) * slab * D);
+      for (int u = 0; u < kBatch; ++u) {
+        w[u] = (s0 + u < S) ? sw[(s0 + u) * kRows + r] : 0.f;
+        raw[u] = bload16(rp, w[u] != 0.f ? off0 + (uint32_t)(s0 + u) * sstep : 0x80000000u);
+      }
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (s0 + u < S)
-        acc += sw[(s0 + u) * kRows + r] * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
+      for (int u = 0; u < kBatch; ++u) acc += w[u] * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
+    }
+  } else {
+    for (int s0 = 0; s0 < S; s0 += kBatch) {
+      u32x4 raw[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (s0 + u < S) raw[u] = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + u) * slab * D);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (s0 + u < S) acc += sw[(s0 + u) * kRows + r] * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
+    }
   }
   const int64_t bh = row / p.sq;
   const int m = (int)(row % p.sq);
@@ -1509,6 +1532,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
     cp.o_bs = kp.o_bs; cp.o_hs = kp.o_hs; cp.o_rs = kp.o_rs;
     cp.b = p->b; cp.h = p->h; cp.sq = p->seqlen_q; cp.num_splits = pl.splits;
     cp.rows = (int64_t)p->b * p->h * p->seqlen_q;
+    cp.part_bytes = pl.o_part_bytes < (1ull << 31) ? (uint32_t)pl.o_part_bytes : 0u;
   }
 
   hipStream_t st = (hipStream_t)stream;
