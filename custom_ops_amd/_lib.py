@@ -27,6 +27,7 @@ EDEVICE = 4
 # Every function include/mi355_fa.h declares (checked by tests/test_host.py).
 EXPORTED = (
     "mi355_fa_fwd",
+    "mi355_fa_fwd_noalloc",
     "mi355_fa_num_splits",
     "mi355_fa_workspace_bytes",
     "mi355_fa_cost_model_splits",
@@ -106,6 +107,8 @@ def load(path: str | None = None) -> ctypes.CDLL:
         P = ctypes.POINTER(Params)
         lib.mi355_fa_fwd.argtypes = [P, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
         lib.mi355_fa_fwd.restype = ctypes.c_int
+        lib.mi355_fa_fwd_noalloc.argtypes = [P, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+        lib.mi355_fa_fwd_noalloc.restype = ctypes.c_int
         lib.mi355_fa_num_splits.argtypes = [P]
         lib.mi355_fa_num_splits.restype = ctypes.c_int
         lib.mi355_fa_workspace_bytes.argtypes = [P]

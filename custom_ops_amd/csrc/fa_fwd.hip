@@ -1550,3 +1550,64 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
 }
 
 }  // extern "C"
+
+// ── entry point that allocates nothing ───────────────────────────────────────
+// mi355_fa_fwd_noalloc keeps the split-KV partials in this file-scope device
+// array instead of a caller workspace: one copy per GPU, resident until the
+// process ends. Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in symbol); it uses the device address that
+// hipGetSymbolAddress returns for the current device, looked up once per
+// device on that device's first call. Partials are fully written before they
+// are read, so nothing needs clearing between calls; calls that overlap on one
+// GPU share the array and race.
+static __device__ __align__(256) unsigned char scratch[MI355_FA_NOALLOC_SCRATCH_BYTES];
+
+static void* g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+static int scratch_of_current_device(void** out, char* err, size_t errlen) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    set_err(err, errlen, "mi355_fa: no current HIP device (%s)", hipGetErrorString(e));
+    return MI355_FA_EDEVICE;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      set_err(err, errlen, "mi355_fa: scratch address lookup failed on device %d: %s", dev,
+              hipGetErrorString(e));
+      return MI355_FA_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MI355_FA_OK;
+}
+
+extern "C" int mi355_fa_fwd_noalloc(const mi355_fa_params* p, void* stream, char* err, size_t errlen) {
+  int rc = validate(p, err, errlen);
+  if (rc) return rc;
+  if (p->b == 0 || p->h == 0 || p->seqlen_q == 0) return MI355_FA_OK;
+  const size_t need = mi355_fa_workspace_bytes(p);
+  if (need > MI355_FA_NOALLOC_SCRATCH_BYTES) {
+    set_err(err, errlen,
+            "split-KV needs %zu bytes of scratch; mi355_fa_fwd_noalloc holds at most %zu "
+            "(use mi355_fa_fwd with a workspace, or fewer splits)",
+            need, (size_t)MI355_FA_NOALLOC_SCRATCH_BYTES);
+    return MI355_FA_EWORKSPACE;
+  }
+  mi355_fa_params q = *p;
+  q.workspace = nullptr;
+  q.workspace_bytes = 0;
+  if (need > 0) {
+    rc = scratch_of_current_device(&q.workspace, err, errlen);
+    if (rc) return rc;
+    q.workspace_bytes = MI355_FA_NOALLOC_SCRATCH_BYTES;
+  }
+  return mi355_fa_fwd(&q, stream, err, errlen);
+}

@@ -86,6 +86,20 @@ typedef struct mi355_fa_params {
  * Returns 0 on success; otherwise writes a NUL-terminated message into err. */
 int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errlen);
 
+/* Size of the per-GPU scratch array behind mi355_fa_fwd_noalloc. */
+#define MI355_FA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20) /* 32 MiB */
+
+/* mi355_fa_fwd without any allocation and without a workspace argument: the
+ * split-KV partials go to a fixed per-GPU device array of
+ * MI355_FA_NOALLOC_SCRATCH_BYTES (allocated when the library's code is loaded
+ * onto a GPU and held until the process ends). p->workspace is ignored. Plans
+ * that need more scratch fail with MI355_FA_EWORKSPACE. Calls that overlap on
+ * one GPU (other streams, other threads) share the array and race: serialise
+ * them. No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+int mi355_fa_fwd_noalloc(const mi355_fa_params* p, void* stream, char* err, size_t errlen);
+
 /* Number of KV splits the launcher will use for these params (after its plan,
  * the MI355_FA_NUM_SPLITS override and clamping). */
 int mi355_fa_num_splits(const mi355_fa_params* p);
