@@ -50,6 +50,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -1277,6 +1278,27 @@ static int pick_pack(const mi355_fa_params* p) {
   return pk;
 }
 
+static int order_head_major(const mi355_fa_params* p, const Plan& pl, int cus) {
+  const char* o = getenv("MI355_FA_ORDER");   // tuning override: "h" or "m"
+  if (o && o[0] == 'h') return 1;
+  if (o && o[0] == 'm') return 0;
+  const double R = (double)(cus / 8 > 0 ? cus / 8 : 1) * (pl.waves == 4 ? 2 : 1);   // workgroups per XCD round
+  const double G = p->h / pl.pack;                                   // head groups (one K/V head each)
+  const double M = ceil_div(p->seqlen_q, pl.block_m / pl.pack);      // m-blocks
+  const double S = pl.splits;
+  const double kv = (double)p->seqlen_k / S * p->d * 4.0;            // K+V of one group, one split
+  const double mk = (double)(pl.block_m / pl.pack) * p->seqlen_k / S * 2.0;   // mask of one m-block, one split
+  auto up = [](double a, double b) { return std::ceil(a / b); };
+  // m-blocks fastest, then splits, then groups: the round's ids cover
+  // ceil(R/M) (group, split) pairs and min(R, M) m-blocks of each split seen
+  const double pairs = std::min(up(R, M), S * G);
+  const double m_fetch = pairs * kv + std::min(R, M) * std::min(S, pairs) * mk;
+  // groups fastest, then m-blocks, then splits: ceil(R/G) (split, m-block)
+  // mask pieces and min(R, G) groups of each split seen
+  const double h_fetch = std::min(up(R, G), M * S) * mk + std::min(R, G) * std::min(S, up(R, G * M)) * kv;
+  return h_fetch < m_fetch ? 1 : 0;
+}
+
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
   pl.pack = pick_pack(p);
@@ -1309,16 +1331,15 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   if (pl.splits < 1) pl.splits = 1;
   const int s = pl.splits;
   pl.block_m = 32 * pl.waves;
-  // Workgroup order. Each XCD runs a contiguous range of tile ids and has its
-  // own L2. With few m-blocks per head, the mask tile (shared by all heads of
-  // a batch) is the stream worth sharing: heads fastest. Otherwise the K/V of
-  // a head (shared by its m-blocks) is: m-blocks fastest.
-  pl.head_major = ceil_div(p->seqlen_q, pl.block_m / pl.pack) <= 2 ? 1 : 0;
-  {
-    const char* o = getenv("MI355_FA_ORDER");   // tuning override: "h" or "m"
-    if (o && o[0] == 'h') pl.head_major = 1;
-    if (o && o[0] == 'm') pl.head_major = 0;
-  }
+  // Workgroup order. Each XCD runs a contiguous range of tile ids with its own
+  // L2 (4 MiB, too small to keep a batch's K/V or mask between rounds), so
+  // what one round of an XCD's workgroups fetches is what counts: the K/V of
+  // the head groups it covers plus the mask rows of the m-blocks it covers.
+  // m-blocks fastest covers few head groups and many m-blocks, heads fastest
+  // the reverse; take the order whose round fetches fewer bytes. (MHA with
+  // long Sq: m-blocks fastest; GQA, whose packed head groups share K/V, and
+  // short Sq: heads fastest.)
+  pl.head_major = order_head_major(p, pl, cus);
   pl.num_m = ceil_div(p->seqlen_q, pl.block_m / pl.pack);
   pl.n_per_split = (s > 1) ? ceil_div(pl.num_n, s) : pl.num_n;
   if (s > 1) {
