@@ -169,6 +169,9 @@ struct KParams {
   int mask_direct;   // mask rows 16-byte aligned: the mask tile can go by LDS DMA
   int head_major;    // tile order: heads fastest (else m-blocks fastest)
   float scale;       // softmax scale (1/sqrt(d) in the reference op)
+  // scale·log2(e) and the rescale slack in score units, as float bits: kernel
+  // arguments arrive in SGPRs, which the assembly loops take as scalar operands
+  uint32_t c2_bits, slack_bits;
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -1048,6 +1051,148 @@ void fa_fwd_kernel_asm(const KParams p) {
   }
 }
 
+// ── ping-pong tile loop in generated assembly (bf16, d = 128) ────────────────
+// fa_fwd_kernel_pp: 8 waves of 32 query rows; waves 0-3 and 4-7 run the same
+// phases one phase apart (one workgroup barrier between phases), so on every
+// SIMD one wave issues an MFMA phase (mask, QK(t), PV(t-1)) while its partner
+// issues a VALU phase (max, exponentials, P, row sums of its tile). K and V
+// have three LDS stages, the mask two (160 KiB); waves 0-3 issue all K/V DMA.
+// The loop is MI355_PP_LOOP_BF16 from gen_fa_loop.py.
+constexpr int kPpKStage = 16384;
+constexpr int kPpVBase = 3 * kPpKStage;
+constexpr int kPpMBase = 6 * kPpKStage;
+constexpr int kPpLds = kPpMBase + 2 * 32768;    // 160 KiB
+
+template <bool SPLIT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fa_fwd_kernel_pp(const KParams p) {
+  constexpr int D = 128;
+  constexpr int UPR = D / 8;
+  __shared__ __align__(16) uint8_t smem[kPpLds];
+  TileIdx ti = tile_index<256>(p);
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  place_wave(ti, p, wave, 32);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const uint16_t* kbase = p.k + (int64_t)ti.b * p.k_bs + (int64_t)ti.hk * p.k_hs;
+  const uint16_t* vbase = p.v + (int64_t)ti.b * p.v_bs + (int64_t)ti.hk * p.v_hs;
+  const uint16_t* mbase = p.mask + (int64_t)ti.b * p.m_bs;
+  const uint32_t kbytes = (uint32_t)p.sk * p.k_rs * 2u, vbytes = (uint32_t)p.sk * p.v_rs * 2u;
+  const uint32_t mbytes = (uint32_t)p.msq * p.m_rs * 2u;
+  const int nb = ti.nb, ne = ti.ne, cnt = ne - nb;
+  const int wa = wave & 3;   // position within the group (group A issues K/V)
+
+  // K/V DMA source of load 0 of group-A wave wa: unit u = wa·64 + lane of the
+  // 64-key tile (rows 16 apart per further load, keys π-permuted per 32)
+  uint32_t koff, voff;
+  {
+    const int u = wa * 64 + lane;
+    const int r = u / UPR, slot = u % UPR;
+    const int key = (r & ~31) + key_perm(r & 31);
+    koff = (uint32_t)(key * p.k_rs + (slot ^ (r % UPR)) * 8) * 2u;
+    voff = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
+  }
+  u32x2 moff;   // this wave's mask rows: loads 0 and 1 (2 and 3 are 16 rows on)
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int m = i * 8 + lane / 8, slot = lane % 8;
+    moff[i] = (uint32_t)((ti.m0 + wave * 32 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
+  }
+  u32x8 krd;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) krd[i] = lds0 + (uint32_t)(l32 * UPR + ((2 * i + g) ^ (l32 % UPR))) * 16u;
+  u32x4 vrd, mrd;
+  {
+    const int s16 = lane & 15, grp = lane >> 4;
+    const int row = 16 * g + s16 / 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int d = 32 * db + 16 * (grp & 1) + 4 * (s16 & 3);
+      vrd[db] = lds0 + kPpVBase + (uint32_t)(row * D * 2 + (((d / 8) ^ v_swz<D>(row)) * 16) + (d % 8) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 4 * (i / 2) + 2 * (i % 2) + g;
+      mrd[i] = lds0 + kPpMBase + (uint32_t)(wave * 32 * 128 + l32 * 128 + ((c ^ mask_swz(l32)) * 16));
+    }
+  }
+  u32x8 msel = {};
+  {
+    const uint32_t sb = (uint32_t)bitcast<uint16_t>((__bf16)(1.f / p.scale));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int e = key_perm(l32) - 16 * c - 8 * g;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) msel[4 * c + w] = (e == 2 * w) ? sb : (e == 2 * w + 1) ? (sb << 16) : 0u;
+    }
+  }
+  const rsrc_t rq = make_rsrc(p.q + (int64_t)ti.b * p.q_bs + (int64_t)ti.h * p.q_hs,
+                              (uint32_t)p.sq * p.q_rs * 2u);
+  u32x32 q[1];
+  {
+    const int qrow = ti.m0 + wave * 32 + l32;
+#pragma unroll
+    for (int kd = 0; kd < 8; ++kd) {
+      const u32x4 v = bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[0][4 * kd + e] = v[e];
+    }
+  }
+  // V rows the last tile's DMA leaves unwritten (Sk % 64) must hold finite values
+  if (p.sk % kBN != 0) {
+    for (int i = tid; i < 3 * kPpKStage / 16; i += 512)
+      reinterpret_cast<u32x4*>(smem + kPpVBase)[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  const uint32_t ksh = (uint32_t)nb * kBN * (uint32_t)p.k_rs * 2u;
+  const uint32_t vsh = (uint32_t)nb * kBN * (uint32_t)p.v_rs * 2u;
+  const uint32_t msh = (uint32_t)nb * kBN * 2u;
+  const uint64_t ka = reinterpret_cast<uint64_t>(kbase) + ksh;
+  const uint64_t va = reinterpret_cast<uint64_t>(vbase) + vsh;
+  const uint64_t ma = reinterpret_cast<uint64_t>(mbase) + msh;
+  auto sgpr = [](uint32_t x) { return __builtin_amdgcn_readfirstlane(x); };
+  const uint32_t klo = sgpr((uint32_t)ka), khi = sgpr((uint32_t)(ka >> 32) & 0xffffu);
+  const uint32_t kn = sgpr(kbytes - ksh);
+  const uint32_t vlo = sgpr((uint32_t)va), vhi = sgpr((uint32_t)(va >> 32) & 0xffffu);
+  const uint32_t vn = sgpr(vbytes - vsh);
+  const uint32_t mlo = sgpr((uint32_t)ma), mhi = sgpr((uint32_t)(ma >> 32) & 0xffffu);
+  const uint32_t mn = sgpr(mbytes - msh);
+  const uint32_t fl = sgpr((uint32_t)kRsrcFlags);
+  const uint32_t kstep = sgpr((uint32_t)kBN * p.k_rs * 2u);
+  const uint32_t vstep = sgpr((uint32_t)kBN * p.v_rs * 2u);
+  const uint32_t k8 = sgpr(8u * p.k_rs * 2u), v16 = sgpr(16u * p.v_rs * 2u), m16 = sgpr(16u * p.m_rs * 2u);
+  const uint32_t lds_k = sgpr(lds0 + (uint32_t)wa * 1024u);
+  const uint32_t lds_v = sgpr(lds0 + (uint32_t)wa * 1024u);   // + kPpVBase in the loop's offsets
+  const uint32_t lds_m = sgpr(lds0 + kPpMBase + (uint32_t)(wave * 32 * 128));
+  const uint32_t lim = sgpr((ne == p.num_n && p.sk % kBN) ? (uint32_t)(p.sk % kBN) : 64u);
+  // host-computed float scalars: kernel arguments, hence SGPRs (a float computed
+  // here in VALU and handed to an "s" operand can arrive as a VGPR inside the
+  // loop's registers, and an explicit readfirstlane right after the VALU write
+  // is a hazard the compiler does not see through inline assembly)
+  const uint32_t c2 = p.c2_bits, slack = p.slack_bits;
+  const uint32_t neginf = sgpr(0xff800000u);
+  const uint32_t mclamp = sgpr(0xff7fff7fu);
+  const uint32_t ntiles = sgpr((uint32_t)cnt);
+  const uint32_t grp = sgpr((uint32_t)(wave >> 2));
+
+  f32x16 o[4];
+  float mrun[1], lsum[1];
+  if (cnt > 0) {
+    asm volatile(MI355_PP_LOOP_BF16 : MI355_PP_OUTPUTS_BF16 : MI355_PP_INPUTS_BF16 : MI355_PP_CLOBBERS_BF16);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+    mrun[0] = -INFINITY;
+    lsum[0] = 0.f;
+  }
+  wait_vmcnt<0>();
+  wg_barrier();
+  const int qrow = ti.m0 + wave * 32 + l32;
+  write_rows<D, true, SPLIT>(p, o, lsum[0], mrun[0], ti.b, ti.h, ti.split, qrow, smem + wave * 8192, lane);
+}
+
 // ── split-KV combine ────────────────────────────────────────────────────────
 struct CParams {
   const uint16_t* o_part;
@@ -1417,7 +1562,9 @@ static hipError_t launch_main(const KParams& kp, hipStream_t st) {
 static int asm_form() {
   static const int f = [] {
     const char* e = getenv("MI355_FA_ASM");
-    return (e && (e[0] == '0' || e[0] == '2')) ? e[0] - '0' : 1;
+    // 3 (default): bf16 runs the ping-pong loop, fp16 the 32-row loop;
+    // 1: the 32-row loop for both; 2: the 64-row loop; 0: the compiled kernel
+    return (e && (e[0] >= '0' && e[0] <= '3')) ? e[0] - '0' : 3;
   }();
   return f;
 }
@@ -1428,7 +1575,9 @@ static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t 
     // bf16 adds the mask on the matrix core, which needs bf16(1/scale) > 1.0078
     // (-max_bf16 · (1/scale) must overflow to -inf): scale < 0.99
     if (pl.waves == 8 && kp.mask_direct && asm_form() && (!BF16 || kp.scale < 0.99f)) {
-      if (asm_form() == 2)
+      if (asm_form() == 3 && BF16)
+        hipLaunchKernelGGL((fa_fwd_kernel_pp<SPLIT>), dim3(kp.total), dim3(512), 0, st, kp);
+      else if (asm_form() == 2)
         hipLaunchKernelGGL((fa_fwd_kernel_asm<2, BF16, SPLIT>), dim3(kp.total), dim3(256), 0, st, kp);
       else
         hipLaunchKernelGGL((fa_fwd_kernel_asm<1, BF16, SPLIT>), dim3(kp.total), dim3(512), 0, st, kp);
@@ -1539,6 +1688,11 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.num_splits = pl.splits; kp.n_per_split = pl.n_per_split;
   kp.total = (int)total;
   kp.scale = p->scale_softmax;
+  {
+    const float c2 = p->scale_softmax * kLog2e, slack = kRescaleSlack / p->scale_softmax;
+    memcpy(&kp.c2_bits, &c2, 4);
+    memcpy(&kp.slack_bits, &slack, 4);
+  }
   kp.head_major = pl.head_major;
   kp.mask_direct = (((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
                     (p->mask_row_stride & 7) == 0) ? 1 : 0;

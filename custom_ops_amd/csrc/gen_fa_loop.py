@@ -120,6 +120,7 @@ W_MFMA_CHAIN = 3      # MFMA result -> the next MFMA accumulating into it
 W_TRANS = 2           # v_exp result -> VALU read
 W_VCC = 3             # VALU write of VCC -> lane-mask read
 W_PERM = 3            # VALU write -> v_permlane32_swap source
+W_DOT = 4             # v_dot2 result -> another VALU's read (the same dot's accumulator: none)
 
 
 class Stream:
@@ -172,13 +173,16 @@ class Load:
     """One LDS read: its text, destination registers and window slot. A slot is
     reused only after every consumer of the previous load in it has issued."""
 
-    def __init__(self, text, dst, slot=None):
+    def __init__(self, text, dst, slot=None, pre=False):
         # the slot is the destination's first register: loads into the same
         # registers (whichever window they belong to) are ordered by it
         self.text, self.dst, self.slot = text, dst, dst[0]
         self.consumers = 0
         self.used = 0
         self.index = None       # position in the issue order
+        # pre: issued (and waited for) before this phase; it only holds its
+        # registers until its consumers here have issued
+        self.pre = pre
 
 
 class Phase:
@@ -239,11 +243,18 @@ class Phase:
                 if id(ld) not in seen:
                     seen.add(id(ld))
                     order.append(ld)
-        last_in_slot = {}
+        # a load may issue once every earlier load whose destination overlaps
+        # its own has been read by all of its consumers
+        last_writer = {}
         prev = {}
         for ld in order:
-            prev[id(ld)] = last_in_slot.get(ld.slot)
-            last_in_slot[ld.slot] = ld
+            prev[id(ld)] = {id(last_writer[r]): last_writer[r] for r in ld.dst if r in last_writer}.values()
+            for r in ld.dst:
+                last_writer[r] = ld
+        for ld in order:
+            if ld.pre:
+                ld.index = -1
+        order = [ld for ld in order if not ld.pre]
         issued = 0
         complete = -1           # loads [0..complete] known landed
 
@@ -251,8 +262,7 @@ class Phase:
             nonlocal issued
             while issued < len(order) and issued - 1 - complete < self.MAXQ:
                 ld = order[issued]
-                pv = prev[id(ld)]
-                if pv is not None and pv.used < pv.consumers:
+                if any(pv.used < pv.consumers for pv in prev[id(ld)]):
                     return
                 ld.index = issued
                 st.emit(ld.text)
@@ -284,14 +294,28 @@ def emit_item(st, v):
             st.emit(line, n)
         return
     if kind == "raw":
+        # a block that may branch over its body counts, as wait states, only
+        # the instructions up to its branch (the body may not execute)
+        start, cut = st.pos, None
         for line in v["lines"]:
             st.emit(line)
+            if cut is None and line.startswith("s_cbranch"):
+                cut = st.pos
+        if cut is not None:
+            st.pos = cut
         return
     reads = v.get("src", [])
     if kind == "mfma":
         st.wait_for(reads, "mfma")
         st.emit(v["text"])
         st.wrote(v.get("dst", []), valu=W_MFMA_VALU, mfma=W_MFMA_CHAIN)
+        return
+    if kind == "dot":               # dst is also the accumulator it reads
+        acc = v["dst"]
+        st.wait_for([r for r in reads if r not in acc], "valu")
+        st.wait_for(acc, "dotacc")
+        st.emit(v["text"])
+        st.wrote(acc, valu=W_DOT, dotacc=0, mfma=W_VALU_MFMA, perm=W_PERM)
         return
     if kind == "vcc_read":
         st.wait_for(["vcc"], "vcc")
@@ -438,7 +462,8 @@ def rowsum_valus(bf16, s_cur):
     for k in range(16):
         for h in range(NH):
             base = S(s_cur, h, 0, 0)
-            out.append(valu(f"{op} v{LSUM + h}, {one}, v{base + k}", [base + k, LSUM + h], [LSUM + h]))
+            out.append(valu(f"{op} v{LSUM + h}, {one}, v{base + k}", [base + k, LSUM + h], [LSUM + h],
+                            kind="dot"))
     return out
 
 
@@ -778,6 +803,346 @@ def gen(bf16: bool, nh: int = 2) -> str:
     return "\n".join(st.lines)
 
 
+# ── ping-pong form (bf16, 8 waves of 32 rows) ────────────────────────────────
+# Waves 0-3 (group A) and 4-7 (group B); wave w and w+4 share a SIMD. Every
+# wave runs the same phases, B one phase behind A, with one workgroup barrier
+# between phases, so while one wave of a SIMD runs an MFMA phase its partner
+# runs a VALU phase:
+#   M_t: mask MFMAs(t) and QK(t) into S[t % 2], then PV(t-1) from P in S[(t-1) % 2]
+#   V_t: tail/max/rescale test of tile t, P(t) = exp2(...) rounded, row sums;
+#        reads (and clamps) mask(t+1) and the first K(t+1) operands for M_{t+1}
+# LDS: K and V in 3 stages each, the mask in 2 (160 KiB). In M_s group A issues
+# K(s+2) and V(s+1) (all K/V DMA of the tile), every wave its own mask rows
+# of tile s+2; that batch is waited for at the end of M_{s+1}.
+PP_KST = 16384
+PP_MST = 32768
+PP_VBASE = 3 * PP_KST
+PP_MBASE = 6 * PP_KST
+PP_LDS = PP_MBASE + 2 * PP_MST      # 160 KiB
+PP_KSLOTS = 6
+PP_VSLOTS = 6
+PP_KPRE = 4                          # K operands read in the V phase before
+PP_DK = (0, 8, 32, 40)               # key offset of K DMA load i (16 rows on, π-permuted)
+
+
+def configure_pp():
+    g = globals()
+    g["NH"] = 1
+    g["WAVES"] = 8
+    g["SBUF"] = 32
+    r = 64
+    g["KWIN"] = r; r += 4 * PP_KSLOTS
+    g["VWIN"] = r; r += 4 * PP_VSLOTS
+    g["MSEL"] = r; r += 8
+    g["K_RD"] = r; r += 8
+    g["V_RD"] = r; r += 4
+    g["M_RD"] = r; r += 4
+    g["K_OFF"] = r; r += 1           # K (and V) DMA source offset of load 0 (group A)
+    g["V_OFF"] = r; r += 1
+    g["M_OFF"] = r; r += 2           # mask DMA offsets of loads 0 and 1 (2, 3: +16 rows)
+    g["MRUN"] = r; r += 1
+    g["MLOG"] = r; r += 1
+    g["LSUM"] = r; r += 1
+    g["T"] = r; r += 7
+    g["NEGINF"] = r; r += 1
+    g["NVGPR"] = r
+    g["QA"] = 0
+    g["OA"] = 32
+    g["NAGPR"] = 96
+    g["WT0"], g["W16G"] = T + 0, T + 1
+    g["TMX"], g["TSW"], g["TTH"] = T + 2, T + 3, T + 4
+    g["TAL"], g["WT1"] = T + 5, T + 6
+
+
+def pp_qk_mfmas(kstage, sbuf):
+    """16 MFMAs of S += K·Qᵀ (accumulating onto the mask MFMAs' result); the
+    first PP_KPRE K operands were read in the V phase before."""
+    out = []
+    for kd in range(KD):
+        for kb in range(2):
+            k = 2 * kd + kb
+            w = KWIN + 4 * (k % PP_KSLOTS)
+            off = kstage * PP_KST + kb * 32 * D * 2
+            ld = Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(K_RD + kd)} offset:{off}", vrange(w, 4),
+                      pre=k < PP_KPRE)
+            dst = S(sbuf, 0, kb, 0)
+            out.append({"kind": "mfma", "needs": [ld],
+                        "text": f"v_mfma_f32_32x32x16_bf16 {vreg(dst, 16)}, {vreg(w, 4)}, "
+                                f"{areg(QA + 4 * kd, 4)}, {vreg(dst, 16)}",
+                        "dst": vrange(dst, 16), "src": vrange(w, 4) + vrange(dst, 16)})
+    return out
+
+
+def pp_k_preread(kstage):
+    """The first PP_KPRE K operand reads of the next M phase (same registers and
+    offsets as pp_qk_mfmas), held by a no-op consumer at the end of the phase."""
+    loads = []
+    for k in range(PP_KPRE):
+        kd, kb = k // 2, k % 2
+        w = KWIN + 4 * (k % PP_KSLOTS)
+        off = kstage * PP_KST + kb * 32 * D * 2
+        loads.append(Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(K_RD + kd)} offset:{off}", vrange(w, 4)))
+    return {"kind": "raw", "lines": [], "needs": loads}
+
+
+PP_MCHUNKS = [(0, 0), (1, 0), (0, 1), (1, 1)]   # (block b, chunk c), issue order
+
+
+def pp_mask_preread(mstage):
+    """mask(t+1) chunks read into the V window and clamped (-inf -> -max_bf16);
+    the M phase's mask MFMAs take them from there."""
+    out = []
+    for idx, (b, c) in enumerate(PP_MCHUNKS):
+        w = VWIN + 4 * idx
+        ld = Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(M_RD + 2 * b + c)} offset:{mstage * PP_MST}", vrange(w, 4))
+        for r in range(4):
+            out.append(valu(f"v_pk_min_u16 v{w + r}, v{w + r}, %[mclamp]", [w + r], [w + r], needs=[ld]))
+    return out
+
+
+def pp_mask_mfmas(sbuf):
+    out = []
+    for idx, (b, c) in enumerate(PP_MCHUNKS):
+        w = VWIN + 4 * idx
+        ld = Load("", vrange(w, 4), pre=True)
+        dst = S(sbuf, 0, b, 0)
+        src_c = "0" if c == 0 else vreg(dst, 16)
+        out.append({"kind": "mfma", "needs": [ld],
+                    "text": f"v_mfma_f32_32x32x16_bf16 {vreg(dst, 16)}, {vreg(MSEL + 4 * c, 4)}, "
+                            f"{vreg(w, 4)}, {src_c}",
+                    "dst": vrange(dst, 16), "src": vrange(w, 4) + (vrange(dst, 16) if c else [])})
+    return out
+
+
+def pp_pv_mfmas(vstage, sbuf):
+    """16 MFMAs of Oᵀ += Vᵀ·Pᵀ, transposed V operands through the V window."""
+    out = []
+    k = 0
+    for j in range(4):
+        for db in range(DB):
+            # slots 4, 5 first: 0-3 hold the mask chunks until the mask MFMAs
+            w = VWIN + 4 * ((k + 4) % PP_VSLOTS)
+            off = vstage * PP_KST + ((j // 2) * 32 + (j % 2) * 8) * D * 2
+            l0 = Load(f"ds_read_b64_tr_b16 {vreg(w, 2)}, {vreg(V_RD + db)} offset:{off}", vrange(w, 2))
+            l1 = Load(f"ds_read_b64_tr_b16 {vreg(w + 2, 2)}, {vreg(V_RD + db)} offset:{off + 4 * D * 2}",
+                      vrange(w + 2, 2))
+            k += 1
+            pr = S(sbuf, 0, 0, 0) + 4 * j
+            o = OA + 16 * db
+            out.append({"kind": "mfma", "needs": [l0, l1],
+                        "text": f"v_mfma_f32_32x32x16_bf16 {areg(o, 16)}, {vreg(w, 4)}, {vreg(pr, 4)}, "
+                                f"{areg(o, 16)}",
+                        "dst": [], "src": vrange(w, 4) + vrange(pr, 4)})
+    return out
+
+
+def pp_dma_items(t_plus2_kstage, t_plus1_vstage, mstage, group_a):
+    """One M phase's DMA: group A all K(t+2) and V(t+1) loads of the workgroup
+    (4 each), every wave its own mask rows of tile t+2. Load i's source offset
+    is load 0's plus a scalar: K rows 16i on (keys PP_DK[i]), V rows 16i on,
+    mask loads 2 and 3 16 rows after 0 and 1. Returns (items, VMEM count)."""
+    items, n = [], 0
+
+    def load(desc, lds, ldsoff, vbase, delta_lines):
+        nonlocal n
+        lines = list(delta_lines)
+        vaddr = f"v{vbase}"
+        if delta_lines:
+            lines += [(f"v_add_u32 v{WT0}, s99, v{vbase}", 1), ("s_nop 1", 2)]
+            vaddr = f"v{WT0}"
+        lines += [(f"s_add_u32 m0, %[{lds}], {ldsoff}", 1), ("s_nop 0", 1),
+                  (f"buffer_load_dwordx4 {vaddr}, s[{desc}:{desc + 3}], 0 offen lds", 1)]
+        items.append({"kind": "other", "lines": lines})
+        n += 1
+
+    def adv(sl, step):
+        items.append({"kind": "other", "lines": [
+            (f"s_add_u32 s{sl}, s{sl}, {step}", 1), (f"s_addc_u32 s{sl + 1}, s{sl + 1}, 0", 1),
+            (f"s_sub_u32 s{sl + 2}, s{sl + 2}, {step}", 1), (f"s_cselect_b32 s{sl + 2}, 0, s{sl + 2}", 1)]})
+
+    def scaled(src, mult):       # s99 = src · mult for mult in 1..5
+        return {1: [(f"s_mov_b32 s99, %[{src}]", 1)],
+                2: [(f"s_lshl_b32 s99, %[{src}], 1", 1)],
+                3: [(f"s_lshl_b32 s99, %[{src}], 1", 1), (f"s_add_u32 s99, s99, %[{src}]", 1)],
+                4: [(f"s_lshl_b32 s99, %[{src}], 2", 1)],
+                5: [(f"s_lshl_b32 s99, %[{src}], 2", 1), (f"s_add_u32 s99, s99, %[{src}]", 1)]}[mult]
+
+    if group_a:
+        for i in range(4):
+            load(80, "lds_k", t_plus2_kstage * PP_KST + i * 4096, K_OFF,
+                 scaled("k8", PP_DK[i] // 8) if i else [])
+        adv(80, "%[kstep]")
+        for i in range(4):
+            load(84, "lds_v", PP_VBASE + t_plus1_vstage * PP_KST + i * 4096, V_OFF,
+                 scaled("v16", i) if i else [])
+        adv(84, "%[vstep]")
+    for i in range(4):
+        load(88, "lds_m", mstage * PP_MST + i * 1024, M_OFF + (i % 2),
+             [(f"s_mov_b32 s99, %[m16]", 1)] if i >= 2 else [])
+    adv(88, "128")
+    return items, n
+
+
+def gen_pp(bf16: bool = True) -> str:
+    """The ping-pong tile loop: common entry and prologue, then one code path
+    per wave group."""
+    assert bf16
+    configure_pp()
+    st = Stream()
+    L = "fa_pp_%="
+    for r in range(32):
+        st.emit(f"v_accvgpr_write_b32 a{QA + r}, v{r}")
+    for r in range(64):
+        st.emit(f"v_accvgpr_write_b32 a{OA + r}, 0")
+    st.emit(f"v_mov_b32 v{MRUN}, %[neginf]")
+    st.emit(f"v_mov_b32 v{MLOG}, 0")
+    st.emit(f"v_mov_b32 v{LSUM}, 0")
+    st.emit(f"v_mov_b32 v{NEGINF}, %[neginf]")
+    st.emit(f"v_mbcnt_lo_u32_b32 v{W16G}, -1, 0")
+    st.emit(f"v_mbcnt_hi_u32_b32 v{W16G}, -1, v{W16G}")
+    st.emit(f"v_lshrrev_b32 v{W16G}, 5, v{W16G}")
+    st.emit(f"v_lshlrev_b32 v{W16G}, 4, v{W16G}")
+    for base, names in ((80, ("klo", "khi", "kn", "fl")), (84, ("vlo", "vhi", "vn", "fl")),
+                        (88, ("mlo", "mhi", "mn", "fl"))):
+        for i, nm in enumerate(names):
+            st.emit(f"s_mov_b32 s{base + i}, %[{nm}]")
+    st.emit("s_mov_b32 s92, %[ntiles]")
+    st.emit("s_sub_u32 s92, s92, 1")             # tiles after the first
+    st.nop(4)
+    st.ready.clear()
+
+    # prologue: K(0), V(0), mask(0) into stage 0, K(1), mask(1) into stage 1
+    # (K/V by group A only), all landed before the common barrier
+    st.emit("s_cmp_eq_u32 %[grp], 0")
+    st.emit(f"s_cbranch_scc0 {L}_pb")
+    pa = []
+    for kst in (0, 1):
+        it, _ = pp_dma_items(kst, 0, kst, True)
+        pa += it[:5] + (it[5:10] if kst == 0 else []) + it[10:]
+    emit_groups(st, pa)
+    st.emit(f"s_branch {L}_pj")
+    st.emit(f"{L}_pb:")
+    pb = []
+    for kst in (0, 1):
+        it, _ = pp_dma_items(0, 0, kst, False)
+        pb += it
+    emit_groups(st, pb)
+    st.emit(f"{L}_pj:")
+    st.emit("s_waitcnt vmcnt(0)")
+    st.emit("s_barrier")
+    st.emit("s_cmp_eq_u32 %[grp], 0")
+    st.emit(f"s_cbranch_scc0 {L}_gb")
+    head = list(st.lines)
+    ga = pp_group(True, L + "_a")
+    gb = pp_group(False, L + "_b")
+    return "\n".join(head + ga + [f"s_branch {L}_end", f"{L}_gb:"] + gb + [f"{L}_end:"] + pp_tail())
+
+
+def pp_tail():
+    st = Stream()
+    st.nop(16)
+    for r in range(64):
+        st.emit(f"v_accvgpr_read_b32 v{r}, a{OA + r}")
+    st.nop(2)
+    return st.lines
+
+
+def pp_group(group_a, L):
+    """One wave group's phases. Group B runs one phase behind group A: it
+    passes one extra barrier first, A one extra at the end."""
+    st = Stream()
+
+    def stamp(k):
+        # timing builds: s_memtime into the debug buffer (4 stamps per tile)
+        if "ppts" not in ABL:
+            return
+        for line in ["s_memtime s[98:99]", "s_waitcnt lgkmcnt(0)", f"v_mov_b32 v{TSW}, s98",
+                     f"v_mov_b32 v{TTH}, s99", f"v_mov_b32 v{WT0}, 0",
+                     f"global_store_dwordx2 v{WT0}, v[{TSW}:{TTH}], s[96:97] offset:{8 * k}"]:
+            st.emit(line)
+        if k == 3:
+            st.emit("s_add_u32 s96, s96, 32")
+            st.emit("s_addc_u32 s97, s97, 0")
+
+    if "ppts" in ABL:
+        st.emit("s_mov_b64 s[96:97], %[dbgp]")
+    if not group_a:
+        st.emit("s_barrier")
+    # operands of M_0: mask(0) clamped, K(0)'s first operands
+    Phase(st).run([], pp_mask_preread(0) + [pp_k_preread(0)])
+
+    def m_phase(t, first, last, prev_batch):
+        """M_t; t is the tile index mod 6 (stages and buffers)."""
+        stamp(0)
+        mf = [] if last else pp_mask_mfmas(t % 2) + pp_qk_mfmas(t % 3, t % 2)
+        if not first:
+            mf += pp_pv_mfmas((t - 1) % 3, (t - 1) % 2)
+        items, n = ([], 0) if last else pp_dma_items((t + 2) % 3, (t + 1) % 3, t % 2, group_a)
+        if "ppnomf" in ABL:      # timing only: no MFMAs (the DMA still runs)
+            mf = []
+        Phase(st).run(mf, [], items)
+        # the batch of the previous M phase has landed (LDS DMA: visible to
+        # the other waves after the barrier)
+        if prev_batch is not None:
+            st.emit(f"s_waitcnt vmcnt({n})")
+        stamp(1)
+        if not (last and not group_a):
+            st.emit("s_barrier")
+        return n
+
+    def v_phase(t, lab):
+        vy = [tail_item(f"{lab}_t", t % 2, left=0)] + max_valus(t % 2)
+        vy.append({"kind": "raw", "lines": rescale_lines(f"{lab}_r")})
+        vy += exp_valus(True, t % 2) + rowsum_valus(True, t % 2)
+        if "ppnovalu" in ABL:    # timing only: the V phase keeps only its reads
+            vy = []
+        vy += pp_mask_preread((t + 1) % 2) + [pp_k_preread((t + 1) % 3)]
+        stamp(2)
+        Phase(st).run([], vy)
+        stamp(3)
+        st.emit("s_barrier")
+
+    m_phase(0, True, False, None)
+    v_phase(0, f"{L}_v0")
+    st.emit("s_cmp_eq_u32 s92, 0")
+    st.emit(f"s_cbranch_scc1 {L}_f0")
+    st.emit(f"{L}_loop:")
+    for r in range(1, 7):
+        t = r % 6
+        m_phase(t, False, False, True)
+        st.emit("s_sub_u32 s92, s92, 1")
+        v_phase(t, f"{L}_v{r}")
+        st.emit("s_cmp_eq_u32 s92, 0")
+        st.emit(f"s_cbranch_scc1 {L}_f{t}")
+    st.emit(f"s_branch {L}_loop")
+    for t in range(6):
+        st.emit(f"{L}_f{t}:")
+        m_phase((t + 1) % 6, False, True, True)
+        st.emit(f"s_branch {L}_x")
+    st.emit(f"{L}_x:")
+    st.emit("s_waitcnt vmcnt(0)")
+    return st.lines
+
+
+def operand_macros_pp():
+    outs = [f'"={{{vreg(16 * i, 16)}}}"(o[{i}])' for i in range(4)]
+    outs += [f'"={{v{MRUN}}}"(mrun[0])', f'"={{v{LSUM}}}"(lsum[0])']
+    ins = [f'"{{{vreg(0, 32)}}}"(q[0])', f'"{{v{K_OFF}}}"(koff)', f'"{{v{V_OFF}}}"(voff)',
+           f'"{{{vreg(M_OFF, 2)}}}"(moff)', f'"{{{vreg(K_RD, 8)}}}"(krd)', f'"{{{vreg(V_RD, 4)}}}"(vrd)',
+           f'"{{{vreg(M_RD, 4)}}}"(mrd)', f'"{{{vreg(MSEL, 8)}}}"(msel)']
+    ins += [f'[{n}] "s"({n})' for n in ("mclamp", "c2", "slack", "neginf", "lim", "lds_k", "lds_v", "lds_m",
+                                         "kstep", "vstep", "k8", "v16", "m16", "klo", "khi", "kn", "vlo",
+                                         "vhi", "vn", "mlo", "mhi", "mn", "fl", "ntiles", "grp")]
+    if "ppts" in ABL:
+        ins.append('[dbgp] "s"(dbgp)')
+    clob = list(range(KWIN, MSEL)) + [MLOG] + list(range(T, NVGPR))
+    cl = [f'"v{r}"' for r in clob] + [f'"a{r}"' for r in range(NAGPR)]
+    cl += [f'"s{r}"' for r in range(80, 100)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
+    return ["#define MI355_PP_OUTPUTS_BF16 " + ", ".join(outs),
+            "#define MI355_PP_INPUTS_BF16 " + ", ".join(ins),
+            "#define MI355_PP_CLOBBERS_BF16 " + ", ".join(cl)]
+
+
 def operand_macros(prefix, bf16):
     """The asm statement's operand lists for one kernel: outputs and inputs
     bound to the physical registers the loop text uses, plus the clobbers."""
@@ -822,6 +1187,13 @@ def render() -> str:
                 parts.append(f'  "{line}\\n\\t" \\')
             parts.append('  ""')
         parts.append(f"// {prefix}: {NVGPR} VGPRs and {NAGPR} AGPRs of the loop's own")
+    text = gen_pp(True)
+    parts += operand_macros_pp()
+    parts.append("#define MI355_PP_LOOP_BF16 \\")
+    for line in text.split("\n"):
+        parts.append(f'  "{line}\\n\\t" \\')
+    parts.append('  ""')
+    parts.append(f"// MI355_PP: {NVGPR} VGPRs and {NAGPR} AGPRs of the loop's own")
     return "\n".join(parts) + "\n"
 
 
