@@ -1,6 +1,8 @@
 """Collect the rocprofv3 evidence for one configuration and write text summaries.
 
     python -m custom_ops_amd.prof_collect --config cfg2 --out prof_out
+    python -m custom_ops_amd.prof_collect --config cfg2 --stall --out prof_out
+    python -m custom_ops_amd.prof_collect --hbm --out prof_out
 
 Runs, each as its own rocprofv3 process under a hard time limit (this process
 never touches the GPU itself):
@@ -45,13 +47,33 @@ PASSES = {
 }
 
 
+# --stall: wave-state counters of the attention kernel (three passes, each
+# within the per-block limits of one rocprofv3 --pmc run)
+STALL_PASSES = {
+    "stall1": ["--pmc", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+               "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_MISC"],
+    "stall2": ["--pmc", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_SCA",
+               "SQ_INST_CYCLES_SALU", "SQ_LDS_IDX_ACTIVE", "SQ_LDS_ADDR_CONFLICT",
+               "SQ_LDS_DATA_FIFO_FULL", "SQ_LDS_CMD_FIFO_FULL"],
+    "stall3": ["--pmc", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_ACTIVE_INST_VALU2",
+               "SQ_LDS_UNALIGNED_STALL", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES",
+               "GRBM_GUI_ACTIVE"],
+}
+HBM_MIB = 2048
+
+
 def workload_cmd(cfg: str, iters: int, bcast: bool = False) -> list[str]:
     return [sys.executable, "-m", "custom_ops_amd.prof_workload", "--config", cfg, "--iters",
             str(iters), "--copy-mib", str(COPY_MIB), *(["--mask-bcast"] if bcast else [])]
 
 
 def rocprof_cmd(name: str, outdir: str, cfg: str, iters: int) -> list[str]:
-    return ["rocprofv3", *PASSES[name], "--output-format", "csv", "-d", outdir, "--",
+    if name == "hbm":
+        return ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", outdir, "--",
+                sys.executable, "-m", "custom_ops_amd.prof_workload", "--hbm-read-mib", str(HBM_MIB),
+                "--iters", str(iters)]
+    args = PASSES.get(name) or STALL_PASSES[name]
+    return ["rocprofv3", *args, "--output-format", "csv", "-d", outdir, "--",
             *workload_cmd(cfg, iters, bcast=name.endswith("_bcast"))]
 
 
@@ -104,17 +126,89 @@ def counter_means(d: str, pred) -> dict[str, float]:
     return {k: sum(v) / len(v) for k, v in acc.items()}
 
 
+def write_summary(path: str, title: str, cmds: list[str], body: list[str]) -> None:
+    lines = [title, "", "commands (run from the repository root; each pass is its own process):"]
+    lines += ["  " + c for c in cmds] + [""] + body
+    txt = "\n".join(lines) + "\n"
+    with open(path, "w") as f:
+        f.write(txt)
+    print(txt, flush=True)
+
+
+def hbm_main(args) -> None:
+    """Cold HBM read ceiling: the probe kernel reading 2 GiB after a 512 MiB
+    flush, per pass; GB/s = bytes / the kernel's average duration."""
+    d = run_pass("hbm", args.out, "", args.iters)
+    stats = rows(d, "kernel_stats.csv")
+    probe = [r for r in stats if "hbm_read_kernel" in r["Name"]]
+    if not probe:
+        raise RuntimeError("no hbm_read_kernel dispatch in the kernel trace")
+    avg_ns = float(probe[0]["AverageNs"])
+    nbytes = HBM_MIB * 1024 * 1024
+    body = ["kernel trace (--stats):",
+            f"  {'name':<60} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9}"]
+    for r in stats:
+        body.append(f"  {r['Name'][:60]:<60} {int(r['Calls']):>6} {float(r['AverageNs'])/1e3:>9.2f} "
+                    f"{float(r['MinNs'])/1e3:>9.2f} {float(r['MaxNs'])/1e3:>9.2f}")
+    body += ["", "derived:",
+             f"  bytes_read_per_pass                {nbytes}",
+             f"  avg_duration_us                    {avg_ns / 1e3:.6g}",
+             f"  min_duration_us                    {float(probe[0]['MinNs']) / 1e3:.6g}",
+             f"  read_gbps_avg                      {nbytes / (avg_ns * 1e-9) / 1e9:.6g}",
+             f"  read_gbps_best                     {nbytes / (float(probe[0]['MinNs']) * 1e-9) / 1e9:.6g}",
+             f"  fraction_of_8TBps                  {nbytes / (avg_ns * 1e-9) / 8e12:.4g}"]
+    write_summary(os.path.join(args.out, "hbm_read_ceiling.txt"),
+                  "# rocprofv3 summary: cold HBM read ceiling (hbm_read_kernel, 2 GiB per pass, "
+                  "512 MiB flush before each)",
+                  [f"python -m custom_ops_amd.prof_collect --hbm --iters {args.iters}",
+                   "cd /tmp && TMPDIR=/tmp PYTHONPATH=<repo> " + " ".join(rocprof_cmd("hbm", "<out>/raw/hbm", "", args.iters))],
+                  body)
+
+
+def stall_main(args, cfg) -> None:
+    """Wave-state counters: where the attention kernel's waves spend their time."""
+    dirs = {p: run_pass(p, args.out, cfg.name, args.iters) for p in STALL_PASSES}
+    m = {}
+    for d in dirs.values():
+        m.update(counter_means(d, is_attn))
+    wc = m["SQ_WAVE_CYCLES"]
+    body = ["counters (mean per dispatch, summed over the device):"]
+    body += [f"  {k:<28} {m[k]:.4g}" for k in sorted(m)]
+    body += ["", "as a share of SQ_WAVE_CYCLES (wave-resident time):"]
+    for k in ("SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_SCA",
+              "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_MISC", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+              "SQ_WAIT_INST_LDS", "SQ_LDS_IDX_ACTIVE"):
+        body.append(f"  {k:<28} {m[k] / wc:.3f}")
+    gui = m["GRBM_GUI_ACTIVE"] / 8
+    body += ["", f"  MFMA busy per SIMD / kernel cycles   {m['SQ_VALU_MFMA_BUSY_CYCLES'] / 1024 / gui:.3f}"]
+    write_summary(os.path.join(args.out, f"stall_fa_fwd_kernel_{cfg.name}.txt"),
+                  f"# rocprofv3 wave-state counters: fa_fwd_kernel on {cfg.name} "
+                  f"(B={cfg.B} H={cfg.H} Hk={cfg.Hk} Sq={cfg.Sq} Sk={cfg.Sk} d={cfg.d})",
+                  [f"python -m custom_ops_amd.prof_collect --config {cfg.name} --stall --iters {args.iters}"]
+                  + ["cd /tmp && TMPDIR=/tmp PYTHONPATH=<repo> timeout -s KILL 90 " +
+                     " ".join(rocprof_cmd(p, f"<out>/raw/{p}", cfg.name, args.iters)) for p in STALL_PASSES],
+                  body)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--out", default=os.path.join(ROOT, "prof_out"))
+    ap.add_argument("--hbm", action="store_true", help="cold HBM read ceiling instead")
+    ap.add_argument("--stall", action="store_true", help="wave-state counters instead")
     args = ap.parse_args()
     args.out = os.path.abspath(args.out)      # the passes run with cwd=/tmp
     os.makedirs(args.out, exist_ok=True)
     sys.path.insert(0, ROOT)
     from custom_ops_amd.workloads import CONFIGS
+    if args.hbm:
+        hbm_main(args)
+        return
     cfg = CONFIGS[args.config]
+    if args.stall:
+        stall_main(args, cfg)
+        return
 
     dirs = {p: run_pass(p, args.out, cfg.name, args.iters) for p in PASSES}
 

@@ -4,6 +4,11 @@ calibration kernel for the FETCH_SIZE / WRITE_SIZE counters).
 
     python -m custom_ops_amd.prof_workload --config cfg2 --iters 20 [--copy-mib 512]
         [--mask-bcast]
+    python -m custom_ops_amd.prof_workload --hbm-read-mib 2048 --iters 20
+
+--hbm-read-mib N measures the cold HBM read ceiling instead: each iteration
+writes a 512 MiB flush buffer (evicting L2 and the 256 MiB last-level cache),
+then the probe kernel (csrc/hbm_probe.hip) reads an N MiB buffer once.
 
 --mask-bcast launches the same call through the C ABI with the mask's row and
 batch strides set to 0: every query row then reads the same (L2-resident)
@@ -29,13 +34,18 @@ def main() -> None:
                     help="mask row/batch strides 0: one L2-resident mask row for every query row")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run 5 copies of a buffer of this many MiB (read N, write N)")
+    ap.add_argument("--hbm-read-mib", type=int, default=0,
+                    help="cold HBM read ceiling: flush, then read a buffer of this many MiB")
     args = ap.parse_args()
 
     import torch
+    dev = torch.device("cuda:0")
+    if args.hbm_read_mib:
+        hbm_read(args.hbm_read_mib, args.iters, dev)
+        return
     from custom_ops_amd import ops
     from custom_ops_amd.workloads import CONFIGS, make_inputs
 
-    dev = torch.device("cuda:0")
     ops.ensure_loaded()
     if args.copy_mib:
         n = args.copy_mib * 1024 * 1024 // 4
@@ -69,6 +79,26 @@ def main() -> None:
         call()
     torch.cuda.synchronize()
     print(f"prof_workload {cfg.name}: {args.iters} launches done", flush=True)
+
+
+def hbm_read(mib: int, iters: int, dev) -> None:
+    import ctypes
+    import torch
+    from custom_ops_amd.build import PROBE_PATH
+    lib = ctypes.CDLL(PROBE_PATH)
+    lib.mi355_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mi355_probe_read.restype = ctypes.c_int
+    buf = torch.ones(mib * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(2048, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for _ in range(iters):
+        flush.fill_(1)
+        rc = lib.mi355_probe_read(buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), stream)
+        if rc:
+            raise RuntimeError(f"mi355_probe_read failed ({rc})")
+    torch.cuda.synchronize()
+    print(f"prof_workload hbm-read {mib} MiB: {iters} passes done", flush=True)
 
 
 if __name__ == "__main__":
