@@ -3,6 +3,7 @@
     python -m custom_ops_amd.prof_collect --config cfg2 --out prof_out
     python -m custom_ops_amd.prof_collect --config cfg2 --stall --out prof_out
     python -m custom_ops_amd.prof_collect --hbm --out prof_out
+    python -m custom_ops_amd.prof_collect --bench --out prof_out
 
 Runs, each as its own rocprofv3 process under a hard time limit (this process
 never touches the GPU itself):
@@ -68,6 +69,9 @@ def workload_cmd(cfg: str, iters: int, bcast: bool = False) -> list[str]:
 
 
 def rocprof_cmd(name: str, outdir: str, cfg: str, iters: int) -> list[str]:
+    if name == "bench":
+        return ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", outdir, "--",
+                sys.executable, os.path.join(ROOT, "bench.py"), "--no-cpu", "--no-configs"]
     if name == "hbm":
         return ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", outdir, "--",
                 sys.executable, "-m", "custom_ops_amd.prof_workload", "--hbm-read-mib", str(HBM_MIB),
@@ -165,6 +169,36 @@ def hbm_main(args) -> None:
                   body)
 
 
+def bench_main(args) -> None:
+    """Kernel trace of bench.py's own timed run (cfg2): the attention kernel's
+    average over every launch, and over the cold steps alone (the launches
+    that directly follow the bench's flush read-back), for comparison with the
+    bench line's event-timed roofline figure."""
+    d = run_pass("bench", args.out, "", 0)
+    stats = rows(d, "kernel_stats.csv")
+    trace = sorted(rows(d, "kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+    cold = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            for i, r in enumerate(trace)
+            if is_attn(r["Kernel_Name"]) and i and "reduce_kernel" in trace[i - 1]["Kernel_Name"]]
+    body = ["kernel trace (--stats):",
+            f"  {'name':<70} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9}"]
+    for r in stats:
+        body.append(f"  {r['Name'][:70]:<70} {int(r['Calls']):>6} {float(r['AverageNs'])/1e3:>9.2f} "
+                    f"{float(r['MinNs'])/1e3:>9.2f} {float(r['MaxNs'])/1e3:>9.2f}")
+    cs = sorted(cold)
+    body += ["", "cold steps (attention launches right after the flush read-back):",
+             f"  count                              {len(cold)}",
+             f"  mean_us                            {sum(cold) / max(1, len(cold)):.6g}",
+             f"  median_us                          {cs[len(cs) // 2] if cs else float('nan'):.6g}",
+             f"  min_us                             {cs[0] if cs else float('nan'):.6g}",
+             f"  max_us                             {cs[-1] if cs else float('nan'):.6g}"]
+    write_summary(os.path.join(args.out, "bench_fa_fwd_kernel_cfg2_trace.txt"),
+                  "# rocprofv3 summary: bench.py --no-cpu --no-configs (cfg2), kernel trace",
+                  ["python -m custom_ops_amd.prof_collect --bench",
+                   "cd /tmp && TMPDIR=/tmp PYTHONPATH=<repo> " + " ".join(rocprof_cmd("bench", "<out>/raw/bench", "", 0))],
+                  body)
+
+
 def stall_main(args, cfg) -> None:
     """Wave-state counters: where the attention kernel's waves spend their time."""
     dirs = {p: run_pass(p, args.out, cfg.name, args.iters) for p in STALL_PASSES}
@@ -197,6 +231,7 @@ def main() -> None:
     ap.add_argument("--out", default=os.path.join(ROOT, "prof_out"))
     ap.add_argument("--hbm", action="store_true", help="cold HBM read ceiling instead")
     ap.add_argument("--stall", action="store_true", help="wave-state counters instead")
+    ap.add_argument("--bench", action="store_true", help="kernel trace of bench.py's timed run instead")
     args = ap.parse_args()
     args.out = os.path.abspath(args.out)      # the passes run with cwd=/tmp
     os.makedirs(args.out, exist_ok=True)
@@ -204,6 +239,9 @@ def main() -> None:
     from custom_ops_amd.workloads import CONFIGS
     if args.hbm:
         hbm_main(args)
+        return
+    if args.bench:
+        bench_main(args)
         return
     cfg = CONFIGS[args.config]
     if args.stall:
