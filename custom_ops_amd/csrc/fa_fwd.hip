@@ -1126,25 +1126,17 @@ void fa_fwd_kernel_pp(const KParams p) {
       for (int w = 0; w < 4; ++w) msel[4 * c + w] = (e == 2 * w) ? sb : (e == 2 * w + 1) ? (sb << 16) : 0u;
     }
   }
-  const rsrc_t rq = make_rsrc(p.q + (int64_t)ti.b * p.q_bs + (int64_t)ti.h * p.q_hs,
-                              (uint32_t)p.sq * p.q_rs * 2u);
-  u32x32 q[1];
-  {
-    const int qrow = ti.m0 + wave * 32 + l32;
-#pragma unroll
-    for (int kd = 0; kd < 8; ++kd) {
-      const u32x4 v = bload16(rq, (uint32_t)(qrow * p.q_rs + kd * 16 + g * 8) * 2u);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) q[0][4 * kd + e] = v[e];
-    }
-  }
-  // V rows the last tile's DMA leaves unwritten (Sk % 64) must hold finite values
+  // Q goes straight from HBM into the loop's AGPRs (the loop issues those
+  // loads with its first tiles' DMA): its buffer and this lane's row offset
+  const uint64_t qa = reinterpret_cast<uint64_t>(p.q + (int64_t)ti.b * p.q_bs + (int64_t)ti.h * p.q_hs);
+  uint32_t qoff = (uint32_t)((ti.m0 + wave * 32 + l32) * p.q_rs + g * 8) * 2u;
+  // V rows the last tile's DMA leaves unwritten (Sk % 64) must hold finite
+  // values: zeroed before any wave's DMA can land in the V stages
   if (p.sk % kBN != 0) {
     for (int i = tid; i < 3 * kPpKStage / 16; i += 512)
       reinterpret_cast<u32x4*>(smem + kPpVBase)[i] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
   }
-  wait_vmcnt<0>();
-  __syncthreads();
 
   const uint32_t ksh = (uint32_t)nb * kBN * (uint32_t)p.k_rs * 2u;
   const uint32_t vsh = (uint32_t)nb * kBN * (uint32_t)p.v_rs * 2u;
@@ -1176,6 +1168,8 @@ void fa_fwd_kernel_pp(const KParams p) {
   const uint32_t mclamp = sgpr(0xff7fff7fu);
   const uint32_t ntiles = sgpr((uint32_t)cnt);
   const uint32_t grp = sgpr((uint32_t)(wave >> 2));
+  const uint32_t qlo = sgpr((uint32_t)qa), qhi = sgpr((uint32_t)(qa >> 32) & 0xffffu);
+  const uint32_t qn = sgpr((uint32_t)p.sq * p.q_rs * 2u);
 
   f32x16 o[4];
   float mrun[1], lsum[1];

@@ -990,8 +990,14 @@ def gen_pp(bf16: bool = True) -> str:
     configure_pp()
     st = Stream()
     L = "fa_pp_%="
-    for r in range(32):
-        st.emit(f"v_accvgpr_write_b32 a{QA + r}, v{r}")
+    # Q straight into its AGPRs (row offset in v[TAL], one 16-d step per
+    # immediate offset); these loads land with the prologue's DMA below, so
+    # the workgroup waits once for both
+    for i, nm in enumerate(("qlo", "qhi", "qn", "fl")):
+        st.emit(f"s_mov_b32 s{92 + i}, %[{nm}]")
+    st.nop(1)
+    for kd in range(KD):
+        st.emit(f"buffer_load_dwordx4 {areg(QA + 4 * kd, 4)}, v{TAL}, s[92:95], 0 offen offset:{kd * 32}")
     for r in range(64):
         st.emit(f"v_accvgpr_write_b32 a{OA + r}, 0")
     st.emit(f"v_mov_b32 v{MRUN}, %[neginf]")
@@ -1126,16 +1132,17 @@ def pp_group(group_a, L):
 
 def operand_macros_pp():
     outs = [f'"={{{vreg(16 * i, 16)}}}"(o[{i}])' for i in range(4)]
-    outs += [f'"={{v{MRUN}}}"(mrun[0])', f'"={{v{LSUM}}}"(lsum[0])']
-    ins = [f'"{{{vreg(0, 32)}}}"(q[0])', f'"{{v{K_OFF}}}"(koff)', f'"{{v{V_OFF}}}"(voff)',
+    outs += [f'"={{v{MRUN}}}"(mrun[0])', f'"={{v{LSUM}}}"(lsum[0])', f'"+{{v{TAL}}}"(qoff)']
+    ins = [f'"{{v{K_OFF}}}"(koff)', f'"{{v{V_OFF}}}"(voff)',
            f'"{{{vreg(M_OFF, 2)}}}"(moff)', f'"{{{vreg(K_RD, 8)}}}"(krd)', f'"{{{vreg(V_RD, 4)}}}"(vrd)',
            f'"{{{vreg(M_RD, 4)}}}"(mrd)', f'"{{{vreg(MSEL, 8)}}}"(msel)']
     ins += [f'[{n}] "s"({n})' for n in ("mclamp", "c2", "slack", "neginf", "lim", "lds_k", "lds_v", "lds_m",
                                          "kstep", "vstep", "k8", "v16", "m16", "klo", "khi", "kn", "vlo",
-                                         "vhi", "vn", "mlo", "mhi", "mn", "fl", "ntiles", "grp")]
+                                         "vhi", "vn", "mlo", "mhi", "mn", "fl", "ntiles", "grp", "qlo",
+                                         "qhi", "qn")]
     if "ppts" in ABL:
         ins.append('[dbgp] "s"(dbgp)')
-    clob = list(range(KWIN, MSEL)) + [MLOG] + list(range(T, NVGPR))
+    clob = list(range(KWIN, MSEL)) + [MLOG] + [r for r in range(T, NVGPR) if r != TAL]
     cl = [f'"v{r}"' for r in clob] + [f'"a{r}"' for r in range(NAGPR)]
     cl += [f'"s{r}"' for r in range(80, 100)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
     return ["#define MI355_PP_OUTPUTS_BF16 " + ", ".join(outs),
