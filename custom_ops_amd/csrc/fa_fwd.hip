@@ -1082,17 +1082,19 @@ void fa_fwd_kernel_pp(const KParams p) {
   const int nb = ti.nb, ne = ti.ne, cnt = ne - nb;
   const int wa = wave & 3;   // position within the group (group A issues K/V)
 
-  // K/V DMA source of load 0 of group-A wave wa: unit u = wa·64 + lane of the
-  // 64-key tile (rows 16 apart per further load, keys π-permuted per 32)
-  uint32_t koff, voff;
-  {
+  // K/V DMA sources of group-A wave wa, loads i = 0, 1: unit u = wa·64 + lane
+  // of a 16-row slice, row r = u/16 + 16i of the 64-key tile (keys π-permuted
+  // per 32); loads 2 and 3 read the same offsets through descriptors 32 rows on
+  u32x2 koff, voff;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
     const int u = wa * 64 + lane;
-    const int r = u / UPR, slot = u % UPR;
+    const int r = u / UPR + 16 * i, slot = u % UPR;
     const int key = (r & ~31) + key_perm(r & 31);
-    koff = (uint32_t)(key * p.k_rs + (slot ^ (r % UPR)) * 8) * 2u;
-    voff = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
+    koff[i] = (uint32_t)(key * p.k_rs + (slot ^ (r % UPR)) * 8) * 2u;
+    voff[i] = (uint32_t)(r * p.v_rs + (slot ^ v_swz<D>(r)) * 8) * 2u;
   }
-  u32x2 moff;   // this wave's mask rows: loads 0 and 1 (2 and 3 are 16 rows on)
+  u32x2 moff;   // this wave's mask rows: 8 per load (loads 2 and 3: 16 rows on, by descriptor)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int m = i * 8 + lane / 8, slot = lane % 8;
@@ -1145,16 +1147,18 @@ void fa_fwd_kernel_pp(const KParams p) {
   const uint64_t va = reinterpret_cast<uint64_t>(vbase) + vsh;
   const uint64_t ma = reinterpret_cast<uint64_t>(mbase) + msh;
   auto sgpr = [](uint32_t x) { return __builtin_amdgcn_readfirstlane(x); };
-  const uint32_t klo = sgpr((uint32_t)ka), khi = sgpr((uint32_t)(ka >> 32) & 0xffffu);
-  const uint32_t kn = sgpr(kbytes - ksh);
-  const uint32_t vlo = sgpr((uint32_t)va), vhi = sgpr((uint32_t)(va >> 32) & 0xffffu);
-  const uint32_t vn = sgpr(vbytes - vsh);
-  const uint32_t mlo = sgpr((uint32_t)ma), mhi = sgpr((uint32_t)(ma >> 32) & 0xffffu);
-  const uint32_t mn = sgpr(mbytes - msh);
-  const uint32_t fl = sgpr((uint32_t)kRsrcFlags);
+  // raw buffer descriptor of `bytes` at `base`, `skip` bytes on (size
+  // saturating at 0); loads 2 and 3 of each tensor use the second one
+  auto desc = [&](uint64_t base, uint32_t bytes, uint32_t skip) {
+    const uint64_t b = base + skip;
+    return u32x4{(uint32_t)sgpr((uint32_t)b), (uint32_t)sgpr((uint32_t)(b >> 32) & 0xffffu),
+                 (uint32_t)sgpr(bytes > skip ? bytes - skip : 0u), (uint32_t)sgpr((uint32_t)kRsrcFlags)};
+  };
+  u32x4 kd0 = desc(ka, kbytes - ksh, 0), kd1 = desc(ka, kbytes - ksh, 32u * p.k_rs * 2u);
+  u32x4 vd0 = desc(va, vbytes - vsh, 0), vd1 = desc(va, vbytes - vsh, 32u * p.v_rs * 2u);
+  u32x4 md0 = desc(ma, mbytes - msh, 0), md1 = desc(ma, mbytes - msh, 16u * p.m_rs * 2u);
   const uint32_t kstep = sgpr((uint32_t)kBN * p.k_rs * 2u);
   const uint32_t vstep = sgpr((uint32_t)kBN * p.v_rs * 2u);
-  const uint32_t k8 = sgpr(8u * p.k_rs * 2u), v16 = sgpr(16u * p.v_rs * 2u), m16 = sgpr(16u * p.m_rs * 2u);
   const uint32_t lds_k = sgpr(lds0 + (uint32_t)wa * 1024u);
   const uint32_t lds_v = sgpr(lds0 + (uint32_t)wa * 1024u);   // + kPpVBase in the loop's offsets
   const uint32_t lds_m = sgpr(lds0 + kPpMBase + (uint32_t)(wave * 32 * 128));
@@ -1168,8 +1172,7 @@ void fa_fwd_kernel_pp(const KParams p) {
   const uint32_t mclamp = sgpr(0xff7fff7fu);
   const uint32_t ntiles = sgpr((uint32_t)cnt);
   const uint32_t grp = sgpr((uint32_t)(wave >> 2));
-  const uint32_t qlo = sgpr((uint32_t)qa), qhi = sgpr((uint32_t)(qa >> 32) & 0xffffu);
-  const uint32_t qn = sgpr((uint32_t)p.sq * p.q_rs * 2u);
+  u32x4 qd = desc(qa, (uint32_t)p.sq * p.q_rs * 2u, 0);
 
   f32x16 o[4];
   float mrun[1], lsum[1];

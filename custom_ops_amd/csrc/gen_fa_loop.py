@@ -435,7 +435,7 @@ def cvt_valus(bf16, s_cur):
     return out
 
 
-def exp_valus(bf16, s_cur):
+def exp_valus(bf16, s_cur, fp32_sum=False):
     """P = exp2(u·c2 - m·c2) rounded to the element type, in place: the P pairs
     of key step j of half h land in S(s_cur, h, 0, 0) + 4j .. +3."""
     cvt = "v_cvt_pk_bf16_f32" if bf16 else "v_cvt_pk_f16_f32"
@@ -448,6 +448,12 @@ def exp_valus(bf16, s_cur):
                 out.append(valu(f"v_fma_f32 v{r}, v{r}, %[c2], -v{MLOG + h}", [r, MLOG + h], [r]))
             for r in regs:
                 out.append(valu(f"v_exp_f32 v{r}, v{r}", [r], [r], kind="trans"))
+            if fp32_sum:
+                # the row sum from the fp32 P, before rounding; v_dot2 over the
+                # packed P would run on the matrix core's datapath, which the
+                # other wave of the SIMD keeps busy
+                for r in regs:
+                    out.append(valu(f"v_add_f32 v{LSUM + h}, v{LSUM + h}, v{r}", [r, LSUM + h], [LSUM + h]))
             for k in range(4):
                 a, b = regs[2 * k], regs[2 * k + 1]
                 dst = base + 4 * grp + k
@@ -837,21 +843,21 @@ def configure_pp():
     g["K_RD"] = r; r += 8
     g["V_RD"] = r; r += 4
     g["M_RD"] = r; r += 4
-    g["K_OFF"] = r; r += 1           # K (and V) DMA source offset of load 0 (group A)
-    g["V_OFF"] = r; r += 1
-    g["M_OFF"] = r; r += 2           # mask DMA offsets of loads 0 and 1 (2, 3: +16 rows)
+    g["K_OFF"] = r; r += 2           # DMA source offsets of K loads 0, 1 (2, 3: second descriptor)
+    g["V_OFF"] = r; r += 2           # V loads 0, 1 (group A; likewise)
+    g["M_OFF"] = r; r += 2           # this wave's mask loads 0, 1 (likewise)
     g["MRUN"] = r; r += 1
     g["MLOG"] = r; r += 1
     g["LSUM"] = r; r += 1
-    g["T"] = r; r += 7
+    g["T"] = r; r += 6
     g["NEGINF"] = r; r += 1
     g["NVGPR"] = r
     g["QA"] = 0
     g["OA"] = 32
     g["NAGPR"] = 96
-    g["WT0"], g["W16G"] = T + 0, T + 1
-    g["TMX"], g["TSW"], g["TTH"] = T + 2, T + 3, T + 4
-    g["TAL"], g["WT1"] = T + 5, T + 6
+    g["W16G"] = T + 0
+    g["TMX"], g["TSW"], g["TTH"] = T + 1, T + 2, T + 3
+    g["TAL"], g["WT1"] = T + 4, T + 5
 
 
 def pp_qk_mfmas(kstage, sbuf):
@@ -885,6 +891,10 @@ def pp_k_preread(kstage):
     return {"kind": "raw", "lines": [], "needs": loads}
 
 
+# experiment: the P conversion and row sum of tile t in the M phase of tile
+# t+1 (slower: the M phase lengthens by more than the V phase shortens)
+P_IN_M = "ppinm" in ABL
+
 PP_MCHUNKS = [(0, 0), (1, 0), (0, 1), (1, 1)]   # (block b, chunk c), issue order
 
 
@@ -914,8 +924,29 @@ def pp_mask_mfmas(sbuf):
     return out
 
 
-def pp_pv_mfmas(vstage, sbuf):
-    """16 MFMAs of Oᵀ += Vᵀ·Pᵀ, transposed V operands through the V window."""
+def pp_p_valus(sbuf):
+    """The P of the previous tile, left in fp32 by its V phase, summed into the
+    row sum and rounded to bf16 pairs in place (key step j lands in
+    S(sbuf) + 4j .. +3, tagged cvt{j} for its PV MFMAs). Runs in the M phase,
+    under this wave's own MFMAs, off the V phase that bounds the tile."""
+    out = []
+    base = S(sbuf, 0, 0, 0)
+    for grp in range(4):
+        regs = [base + 8 * grp + e for e in range(8)]
+        for r in regs:
+            out.append(valu(f"v_add_f32 v{LSUM}, v{LSUM}, v{r}", [r, LSUM], [LSUM]))
+        for k in range(4):
+            a, b = regs[2 * k], regs[2 * k + 1]
+            it = valu(f"v_cvt_pk_bf16_f32 v{base + 4 * grp + k}, v{a}, v{b}", [a, b], [base + 4 * grp + k])
+            it["tag"] = f"cvt{grp}"
+            out.append(it)
+    return out
+
+
+def pp_pv_mfmas(vstage, sbuf, p_here=False):
+    """16 MFMAs of Oᵀ += Vᵀ·Pᵀ, transposed V operands through the V window
+    (p_here: key step j's P is converted in this phase, by the items tagged
+    cvt{j})."""
     out = []
     k = 0
     for j in range(4):
@@ -933,26 +964,24 @@ def pp_pv_mfmas(vstage, sbuf):
                         "text": f"v_mfma_f32_32x32x16_bf16 {areg(o, 16)}, {vreg(w, 4)}, {vreg(pr, 4)}, "
                                 f"{areg(o, 16)}",
                         "dst": [], "src": vrange(w, 4) + vrange(pr, 4)})
+            if p_here:
+                out[-1]["deps"] = (f"cvt{j}",)
     return out
 
 
-def pp_dma_items(t_plus2_kstage, t_plus1_vstage, mstage, group_a):
+def pp_dma_items(t_plus2_kstage, t_plus1_vstage, mstage, group_a, parts="kvm"):
     """One M phase's DMA: group A all K(t+2) and V(t+1) loads of the workgroup
-    (4 each), every wave its own mask rows of tile t+2. Load i's source offset
-    is load 0's plus a scalar: K rows 16i on (keys PP_DK[i]), V rows 16i on,
-    mask loads 2 and 3 16 rows after 0 and 1. Returns (items, VMEM count)."""
+    (4 each), every wave its own mask rows of tile t+2; parts selects K, V
+    and mask. Every load has its source offset in a register of its own
+    (fixed per lane; the descriptor base moves one tile per batch), and its M0
+    write is a separate item, so the phase scheduler puts an MFMA between the
+    two instead of a wait state. Returns (items, VMEM count)."""
     items, n = [], 0
 
-    def load(desc, lds, ldsoff, vbase, delta_lines):
+    def load(desc, lds, ldsoff, voff):
         nonlocal n
-        lines = list(delta_lines)
-        vaddr = f"v{vbase}"
-        if delta_lines:
-            lines += [(f"v_add_u32 v{WT0}, s99, v{vbase}", 1), ("s_nop 1", 2)]
-            vaddr = f"v{WT0}"
-        lines += [(f"s_add_u32 m0, %[{lds}], {ldsoff}", 1), ("s_nop 0", 1),
-                  (f"buffer_load_dwordx4 {vaddr}, s[{desc}:{desc + 3}], 0 offen lds", 1)]
-        items.append({"kind": "other", "lines": lines})
+        items.append({"kind": "m0", "lines": [(f"s_add_u32 m0, %[{lds}], {ldsoff}", 1)]})
+        items.append({"kind": "dma", "lines": [(f"buffer_load_dwordx4 v{voff}, s[{desc}:{desc + 3}], 0 offen lds", 1)]})
         n += 1
 
     def adv(sl, step):
@@ -960,26 +989,26 @@ def pp_dma_items(t_plus2_kstage, t_plus1_vstage, mstage, group_a):
             (f"s_add_u32 s{sl}, s{sl}, {step}", 1), (f"s_addc_u32 s{sl + 1}, s{sl + 1}, 0", 1),
             (f"s_sub_u32 s{sl + 2}, s{sl + 2}, {step}", 1), (f"s_cselect_b32 s{sl + 2}, 0, s{sl + 2}", 1)]})
 
-    def scaled(src, mult):       # s99 = src · mult for mult in 1..5
-        return {1: [(f"s_mov_b32 s99, %[{src}]", 1)],
-                2: [(f"s_lshl_b32 s99, %[{src}], 1", 1)],
-                3: [(f"s_lshl_b32 s99, %[{src}], 1", 1), (f"s_add_u32 s99, s99, %[{src}]", 1)],
-                4: [(f"s_lshl_b32 s99, %[{src}], 2", 1)],
-                5: [(f"s_lshl_b32 s99, %[{src}], 2", 1), (f"s_add_u32 s99, s99, %[{src}]", 1)]}[mult]
-
-    if group_a:
-        for i in range(4):
-            load(80, "lds_k", t_plus2_kstage * PP_KST + i * 4096, K_OFF,
-                 scaled("k8", PP_DK[i] // 8) if i else [])
-        adv(80, "%[kstep]")
-        for i in range(4):
-            load(84, "lds_v", PP_VBASE + t_plus1_vstage * PP_KST + i * 4096, V_OFF,
-                 scaled("v16", i) if i else [])
-        adv(84, "%[vstep]")
+    # loads 2 and 3 of each tensor use its second descriptor (s68 K, s72 V,
+    # s76 mask), whose base is 32 keys / 32 rows / 16 mask rows on
+    if group_a and "ppnokv" not in ABL:   # (ppnokv: timing only, no K/V DMA)
+        if "k" in parts:
+            for i in range(4):
+                load(80 if i < 2 else 68, "lds_k", t_plus2_kstage * PP_KST + i * 4096, K_OFF + i % 2)
+            adv(80, "%[kstep]")
+            adv(68, "%[kstep]")
+        if "v" in parts:
+            for i in range(4):
+                load(84 if i < 2 else 72, "lds_v", PP_VBASE + t_plus1_vstage * PP_KST + i * 4096,
+                     V_OFF + i % 2)
+            adv(84, "%[vstep]")
+            adv(72, "%[vstep]")
+    if "ppnomdma" in ABL or "ppnomask" in ABL or "m" not in parts:   # (timing only: no mask DMA)
+        return items, n
     for i in range(4):
-        load(88, "lds_m", mstage * PP_MST + i * 1024, M_OFF + (i % 2),
-             [(f"s_mov_b32 s99, %[m16]", 1)] if i >= 2 else [])
+        load(88 if i < 2 else 76, "lds_m", mstage * PP_MST + i * 1024, M_OFF + i % 2)
     adv(88, "128")
+    adv(76, "128")
     return items, n
 
 
@@ -993,9 +1022,6 @@ def gen_pp(bf16: bool = True) -> str:
     # Q straight into its AGPRs (row offset in v[TAL], one 16-d step per
     # immediate offset); these loads land with the prologue's DMA below, so
     # the workgroup waits once for both
-    for i, nm in enumerate(("qlo", "qhi", "qn", "fl")):
-        st.emit(f"s_mov_b32 s{92 + i}, %[{nm}]")
-    st.nop(1)
     for kd in range(KD):
         st.emit(f"buffer_load_dwordx4 {areg(QA + 4 * kd, 4)}, v{TAL}, s[92:95], 0 offen offset:{kd * 32}")
     for r in range(64):
@@ -1008,10 +1034,6 @@ def gen_pp(bf16: bool = True) -> str:
     st.emit(f"v_mbcnt_hi_u32_b32 v{W16G}, -1, v{W16G}")
     st.emit(f"v_lshrrev_b32 v{W16G}, 5, v{W16G}")
     st.emit(f"v_lshlrev_b32 v{W16G}, 4, v{W16G}")
-    for base, names in ((80, ("klo", "khi", "kn", "fl")), (84, ("vlo", "vhi", "vn", "fl")),
-                        (88, ("mlo", "mhi", "mn", "fl"))):
-        for i, nm in enumerate(names):
-            st.emit(f"s_mov_b32 s{base + i}, %[{nm}]")
     st.emit("s_mov_b32 s92, %[ntiles]")
     st.emit("s_sub_u32 s92, s92, 1")             # tiles after the first
     st.nop(4)
@@ -1023,8 +1045,8 @@ def gen_pp(bf16: bool = True) -> str:
     st.emit(f"s_cbranch_scc0 {L}_pb")
     pa = []
     for kst in (0, 1):
-        it, _ = pp_dma_items(kst, 0, kst, True)
-        pa += it[:5] + (it[5:10] if kst == 0 else []) + it[10:]
+        it, _ = pp_dma_items(kst, 0, kst, True, parts="kvm" if kst == 0 else "km")
+        pa += it
     emit_groups(st, pa)
     st.emit(f"s_branch {L}_pj")
     st.emit(f"{L}_pb:")
@@ -1063,8 +1085,8 @@ def pp_group(group_a, L):
         if "ppts" not in ABL:
             return
         for line in ["s_memtime s[98:99]", "s_waitcnt lgkmcnt(0)", f"v_mov_b32 v{TSW}, s98",
-                     f"v_mov_b32 v{TTH}, s99", f"v_mov_b32 v{WT0}, 0",
-                     f"global_store_dwordx2 v{WT0}, v[{TSW}:{TTH}], s[96:97] offset:{8 * k}"]:
+                     f"v_mov_b32 v{TTH}, s99", f"v_mov_b32 v{TAL}, 0",
+                     f"global_store_dwordx2 v{TAL}, v[{TSW}:{TTH}], s[96:97] offset:{8 * k}"]:
             st.emit(line)
         if k == 3:
             st.emit("s_add_u32 s96, s96, 32")
@@ -1081,12 +1103,15 @@ def pp_group(group_a, L):
         """M_t; t is the tile index mod 6 (stages and buffers)."""
         stamp(0)
         mf = [] if last else pp_mask_mfmas(t % 2) + pp_qk_mfmas(t % 3, t % 2)
+        pv = []
         if not first:
-            mf += pp_pv_mfmas((t - 1) % 3, (t - 1) % 2)
+            mf += pp_pv_mfmas((t - 1) % 3, (t - 1) % 2, p_here=P_IN_M)
+            if P_IN_M:
+                pv = pp_p_valus((t - 1) % 2)
         items, n = ([], 0) if last else pp_dma_items((t + 2) % 3, (t + 1) % 3, t % 2, group_a)
         if "ppnomf" in ABL:      # timing only: no MFMAs (the DMA still runs)
             mf = []
-        Phase(st).run(mf, [], items)
+        Phase(st).run(mf, pv, items)
         # the batch of the previous M phase has landed (LDS DMA: visible to
         # the other waves after the barrier)
         if prev_batch is not None:
@@ -1099,10 +1124,17 @@ def pp_group(group_a, L):
     def v_phase(t, lab):
         vy = [tail_item(f"{lab}_t", t % 2, left=0)] + max_valus(t % 2)
         vy.append({"kind": "raw", "lines": rescale_lines(f"{lab}_r")})
-        vy += exp_valus(True, t % 2) + rowsum_valus(True, t % 2)
+        if P_IN_M:               # P stays fp32 until the next M phase
+            vy += exp_only_valus(t % 2)
+        elif "ppdot" in ABL:     # row sum by v_dot2 over the bf16 P
+            vy += exp_valus(True, t % 2) + rowsum_valus(True, t % 2)
+        else:
+            vy += exp_valus(True, t % 2, fp32_sum=True)
         if "ppnovalu" in ABL:    # timing only: the V phase keeps only its reads
             vy = []
-        vy += pp_mask_preread((t + 1) % 2) + [pp_k_preread((t + 1) % 3)]
+        if "ppnomask" not in ABL:   # (ppnomask: timing only, no mask reads)
+            vy += pp_mask_preread((t + 1) % 2)
+        vy += [pp_k_preread((t + 1) % 3)]
         stamp(2)
         Phase(st).run([], vy)
         stamp(3)
@@ -1133,18 +1165,19 @@ def pp_group(group_a, L):
 def operand_macros_pp():
     outs = [f'"={{{vreg(16 * i, 16)}}}"(o[{i}])' for i in range(4)]
     outs += [f'"={{v{MRUN}}}"(mrun[0])', f'"={{v{LSUM}}}"(lsum[0])', f'"+{{v{TAL}}}"(qoff)']
-    ins = [f'"{{v{K_OFF}}}"(koff)', f'"{{v{V_OFF}}}"(voff)',
+    # buffer descriptors bound to their SGPR quads (the loop advances them)
+    outs += [f'"+{{s[{b}:{b + 3}]}}"({n})' for b, n in ((80, "kd0"), (68, "kd1"), (84, "vd0"), (72, "vd1"),
+                                                         (88, "md0"), (76, "md1"), (92, "qd"))]
+    ins = [f'"{{{vreg(K_OFF, 2)}}}"(koff)', f'"{{{vreg(V_OFF, 2)}}}"(voff)',
            f'"{{{vreg(M_OFF, 2)}}}"(moff)', f'"{{{vreg(K_RD, 8)}}}"(krd)', f'"{{{vreg(V_RD, 4)}}}"(vrd)',
            f'"{{{vreg(M_RD, 4)}}}"(mrd)', f'"{{{vreg(MSEL, 8)}}}"(msel)']
     ins += [f'[{n}] "s"({n})' for n in ("mclamp", "c2", "slack", "neginf", "lim", "lds_k", "lds_v", "lds_m",
-                                         "kstep", "vstep", "k8", "v16", "m16", "klo", "khi", "kn", "vlo",
-                                         "vhi", "vn", "mlo", "mhi", "mn", "fl", "ntiles", "grp", "qlo",
-                                         "qhi", "qn")]
+                                         "kstep", "vstep", "ntiles", "grp")]
     if "ppts" in ABL:
         ins.append('[dbgp] "s"(dbgp)')
     clob = list(range(KWIN, MSEL)) + [MLOG] + [r for r in range(T, NVGPR) if r != TAL]
     cl = [f'"v{r}"' for r in clob] + [f'"a{r}"' for r in range(NAGPR)]
-    cl += [f'"s{r}"' for r in range(80, 100)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
+    cl += [f'"s{r}"' for r in range(96, 100)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
     return ["#define MI355_PP_OUTPUTS_BF16 " + ", ".join(outs),
             "#define MI355_PP_INPUTS_BF16 " + ", ".join(ins),
             "#define MI355_PP_CLOBBERS_BF16 " + ", ".join(cl)]
