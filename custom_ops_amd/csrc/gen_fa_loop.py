@@ -52,6 +52,9 @@ OUT = os.path.join(HERE, "fa_loop.inc")
 # timestamps into a debug buffer whose address the scratch build binds to
 # v[231:232])
 ABL = set(filter(None, os.environ.get("W64_ABLATE", "").split(",")))
+BAL = "nobal" not in ABL             # 64-row bf16 loop: cost-balanced tile body
+BAL_BUDGET = next((int(a[3:]) for a in ABL if a.startswith("bud")), 28)   # VALU cycles per MFMA
+FP32_SUM = "dotsum" not in ABL       # row sums by v_add over fp32 P (dotsum: by v_dot2)
 PRIO_STEPS = next((int(a[4:]) for a in ABL if a.startswith("prio")), 0)
 
 D = 128
@@ -77,7 +80,7 @@ def configure(nh):
     r = 2 * SBUF
     g["KWIN"] = r; r += 16               # K operand window, 4 slots
     g["VWIN"] = r; r += 16               # V operand window, 4 slots
-    g["MWIN"] = r; r += 8                # mask window, 2 slots of 4
+    g["MWIN"] = r; r += 32 if (nh == 2 and BAL) else 8   # mask window, slots of 4
     g["MSEL"] = r; r += 8                # bf16 mask selectors A_0, A_1
     g["NKL"] = 16 // WAVES               # K (and V) DMA loads per wave per tile
     g["NML"] = 4 * nh                    # mask DMA loads per wave per tile
@@ -104,6 +107,8 @@ def configure(nh):
     g["TAL"], g["WT1"] = T + 2 + 3 * nh, T + 3 + 3 * nh
     # bf16 mask chunks in flight: the mask window plus (idle during PV) K window
     g["MSLOTS"] = [MWIN, MWIN + 4, KWIN, KWIN + 4, KWIN + 8, KWIN + 12][:6 if nh == 2 else 4]
+    if nh == 2 and BAL:     # the balanced body: one slot per chunk (the K window is busy)
+        g["MSLOTS"] = [MWIN + 4 * i for i in range(8)]
     g["NSLOT"] = len(MSLOTS)
 
 
@@ -200,7 +205,10 @@ class Phase:
     def __init__(self, st):
         self.st = st
 
-    def run(self, mfmas, valus, others=(), valu_lead=0):
+    def run(self, mfmas, valus, others=(), valu_lead=0, exact=False, others_span=None):
+        """exact: every VALU item carries the MFMA slot it follows (min_mfma,
+        -1 = before the first MFMA) and goes exactly there; others_span: the
+        scalar/DMA items spread over the first that many MFMAs only."""
         st = self.st
         if "nolds" in ABL:
             mfmas = [dict(m, needs=[]) for m in mfmas]
@@ -209,7 +217,10 @@ class Phase:
         valus, others = list(valus), list(others)
         nm = len(mfmas)
         per = (len(valus) - valu_lead + nm - 1) // nm if nm else 0
-        oper = (len(others) + nm - 1) // nm if nm else 0
+        if exact:
+            per, valu_lead = len(valus), len(valus)
+        span = min(nm, others_span or nm)
+        oper = (len(others) + span - 1) // span if nm else 0
         oi = 0
         vi = 0
 
@@ -404,8 +415,10 @@ def pv_mfmas(bf16, vstage_off, s_cur):
     return out
 
 
-def exp_only_valus(s_cur):
-    """exp2(u·c2 - m·c2) in place, fp32 (converted to P in Y by cvt_valus)."""
+def exp_only_valus(s_cur, fp32_sum=False):
+    """exp2(u·c2 - m·c2) in place, fp32 (converted to P in Y by cvt_valus);
+    fp32_sum: the row sums taken from these fp32 values (v_dot2 over the
+    packed P would wait on the matrix core, busy with this wave's MFMAs)."""
     out = []
     for grp in range(4):
         for h in range(NH):
@@ -415,6 +428,9 @@ def exp_only_valus(s_cur):
                 out.append(valu(f"v_fma_f32 v{r}, v{r}, %[c2], -v{MLOG + h}", [r, MLOG + h], [r]))
             for r in regs:
                 out.append(valu(f"v_exp_f32 v{r}, v{r}", [r], [r], kind="trans"))
+            if fp32_sum:
+                for r in regs:
+                    out.append(valu(f"v_add_f32 v{LSUM + h}, v{LSUM + h}, v{r}", [r, LSUM + h], [LSUM + h]))
     return out
 
 
@@ -647,6 +663,59 @@ def emit_groups(st, items):
         emit_item(st, it)
 
 
+# issue cost (cycles, one wave) of a VALU item when planning slots
+def valu_cost(it):
+    if it.get("kind") == "raw":
+        return 0
+    if it.get("kind") == "trans":
+        return 8
+    if it.get("kind") == "perm":
+        return 10
+    return 5
+
+
+def plan_slots(nm, queues, budget):
+    """Assign each VALU item the MFMA slot it follows (-1: before the first).
+    queues: ordered lists of items, each item optionally with 'earliest' (slot)
+    and 'deadline' (the MFMA index it must precede). Slot by slot, the item whose
+    queue has the nearest deadline goes first while the slot's cost budget
+    lasts; an item past its deadline's last slot goes anyway. Returns the
+    items in issue order, each with min_mfma set."""
+    qs = [list(q) for q in queues]
+    out = []
+    for slot in range(-1, nm):
+        used = 0
+        while True:
+            best, key = None, None
+            for qi, q in enumerate(qs):
+                if not q or q[0].get("earliest", -1) > slot:
+                    continue
+                # urgency: cost left up to the queue's next deadline per slot left
+                k_dl = next((k for k, it in enumerate(q) if "deadline" in it), None)
+                dl = q[k_dl]["deadline"] if k_dl is not None else nm
+                todo = sum(valu_cost(it) for it in q[:(k_dl + 1) if k_dl is not None else len(q)])
+                urg = todo / max(1, dl - slot)
+                forced = k_dl is not None and dl - 1 <= slot
+                k = (0 if forced else 1, -urg, qi)
+                if key is None or k < key:
+                    best, key = qi, k
+            if best is None:
+                break
+            it = qs[best][0]
+            c = valu_cost(it)
+            if used + c > budget and key[0] == 1 and slot < nm - 1:
+                break
+            qs[best].pop(0)
+            it["min_mfma"] = slot
+            used += c
+            out.append(it)
+    for q in qs:
+        for it in q:
+            it["min_mfma"] = nm - 1
+            out.append(it)
+    return out
+
+
 def gen(bf16: bool, nh: int = 2) -> str:
     configure(nh)
     st = Stream()
@@ -733,8 +802,9 @@ def gen(bf16: bool, nh: int = 2) -> str:
             st.emit(f"s_setprio {PRIO_STEPS - 1}")
         stamp(0)
         if last:
-            Phase(st).run([], exp_only_valus(p))
-            Phase(st).run(pv_mfmas(bf16, V_LDS + p * KSTAGE, p), cvt_valus(bf16, p) + rowsum_valus(bf16, p))
+            Phase(st).run([], exp_only_valus(p, fp32_sum=FP32_SUM))
+            Phase(st).run(pv_mfmas(bf16, V_LDS + p * KSTAGE, p),
+                          cvt_valus(bf16, p) + ([] if FP32_SUM else rowsum_valus(bf16, p)))
             return
         # tile n+2's K and mask into stage p (out of range past the last tile),
         # tile n+1's V into stage 1-p: single instructions spread over the tile
@@ -745,7 +815,11 @@ def gen(bf16: bool, nh: int = 2) -> str:
         # so V and mask reads of PV prefetch under the end of QK.
         qk = [] if "noqk" in ABL else qk_mfmas(bf16, K_LDS + nxt * KSTAGE, nxt)
         pv = [] if "nopv" in ABL else pv_mfmas(bf16, V_LDS + p * KSTAGE, p)
-        ex = [] if "noexp" in ABL else exp_only_valus(p)
+        ex = [] if "noexp" in ABL else exp_only_valus(p, fp32_sum=FP32_SUM)
+        rs = [] if FP32_SUM else rowsum_valus(bf16, p)
+        if bf16 and NH == 2 and BAL:
+            balanced_body(st, qk, pv, ex, others, nxt, lab)
+            return
         if bf16:
             mm, clamps = mask_mfma_items(nxt, M_LDS + nxt * MSTAGE)
             mfy = []
@@ -764,18 +838,56 @@ def gen(bf16: bool, nh: int = 2) -> str:
             late = [tail_item(f"{lab}_t", nxt, left=2)] + max_valus(nxt)
             for it in late:
                 it["min_mfma"] = mpos[-1]
-            vy = interleave(cvt_valus(bf16, p), clamps) + rowsum_valus(bf16, p) + late
+            vy = interleave(cvt_valus(bf16, p), clamps) + rs + late
         else:
             mf = qk + pv
             late = mask_add_valus(bf16, nxt, M_LDS + nxt * MSTAGE) + \
                 [tail_item(f"{lab}_t", nxt, left=2)] + max_valus(nxt)
             for it in late:     # they read the QK results: after the last QK MFMA
                 it["min_mfma"] = len(qk) - 1
-            vy = cvt_valus(bf16, p) + rowsum_valus(bf16, p) + late
+            vy = cvt_valus(bf16, p) + rs + late
         if "novaluy" in ABL:
             vy = [{"kind": "raw", "lines": ["s_mov_b64 s[94:95], 0"]}]
         start = len(st.lines)
         Phase(st).run(mf, ex + vy, others, valu_lead=0 if "noexp" in ABL else 8)
+        prio_steps(start, len(mf))
+        st.emit("s_sub_u32 s92, s92, 1")
+        stamp(1)
+        stamp(2)
+        for line in rescale_lines(f"{lab}_r"):
+            st.emit(line)
+        stamp(3)
+        st.ready.clear()
+
+    def balanced_body(st, qk, pv, ex, others, nxt, lab):
+        """MFMAs: QK(n+1) kd 0-3, the mask of n+1, QK(n+1) kd 4-7, PV(n). VALU,
+        placed by cost (plan_slots): the mask clamps first (each before its mask
+        MFMA), then exp/row sums/conversion of n group by group (conversion j
+        before PV step j), the tail and row max of n+1 once S(n+1) is final.
+        The tile's DMA issues under the first half of the MFMAs."""
+        p = 1 - nxt
+        mm, clamps = mask_mfma_items(nxt, M_LDS + nxt * MSTAGE)
+        mf = qk[:16] + mm + qk[16:] + pv
+        for idx in range(len(mm)):
+            for it in clamps[4 * idx:4 * idx + 4]:
+                it["deadline"] = 16 + idx
+        cv = cvt_valus(bf16, p)
+        chain = []
+        per_grp = len(ex) // 4
+        for j in range(4):
+            chain += ex[per_grp * j:per_grp * (j + 1)]
+            grp = [it for it in cv if it.get("tag") == f"cvt{j}"]
+            for it in grp:
+                it["deadline"] = 40 + 8 * j
+            chain += grp
+        late = [tail_item(f"{lab}_t", nxt, left=2)] + max_valus(nxt)
+        for it in late:
+            it["earliest"] = 40
+        vy = plan_slots(len(mf), [clamps, chain, late], BAL_BUDGET)
+        if "novaluy" in ABL:
+            vy = [{"kind": "raw", "lines": ["s_mov_b64 s[94:95], 0"]}]
+        start = len(st.lines)
+        Phase(st).run(mf, vy, others, exact=True, others_span=36)
         prio_steps(start, len(mf))
         st.emit("s_sub_u32 s92, s92, 1")
         stamp(1)
@@ -872,7 +984,9 @@ def pp_qk_mfmas(kstage, sbuf):
             ld = Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(K_RD + kd)} offset:{off}", vrange(w, 4),
                       pre=k < PP_KPRE)
             dst = S(sbuf, 0, kb, 0)
-            out.append({"kind": "mfma", "needs": [ld],
+            if "ppnokr" in ABL:   # timing only: no K reads, the A operand real (V window) data
+                w = VWIN + 4 * (k % PP_VSLOTS)
+            out.append({"kind": "mfma", "needs": [] if ("ppnok" in ABL or "ppnokr" in ABL) else [ld],
                         "text": f"v_mfma_f32_32x32x16_bf16 {vreg(dst, 16)}, {vreg(w, 4)}, "
                                 f"{areg(QA + 4 * kd, 4)}, {vreg(dst, 16)}",
                         "dst": vrange(dst, 16), "src": vrange(w, 4) + vrange(dst, 16)})
@@ -888,7 +1002,7 @@ def pp_k_preread(kstage):
         w = KWIN + 4 * (k % PP_KSLOTS)
         off = kstage * PP_KST + kb * 32 * D * 2
         loads.append(Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(K_RD + kd)} offset:{off}", vrange(w, 4)))
-    return {"kind": "raw", "lines": [], "needs": loads}
+    return {"kind": "raw", "lines": [], "needs": [] if ("ppnok" in ABL or "ppnokr" in ABL) else loads}
 
 
 # experiment: the P conversion and row sum of tile t in the M phase of tile
@@ -957,10 +1071,15 @@ def pp_pv_mfmas(vstage, sbuf, p_here=False):
             l0 = Load(f"ds_read_b64_tr_b16 {vreg(w, 2)}, {vreg(V_RD + db)} offset:{off}", vrange(w, 2))
             l1 = Load(f"ds_read_b64_tr_b16 {vreg(w + 2, 2)}, {vreg(V_RD + db)} offset:{off + 4 * D * 2}",
                       vrange(w + 2, 2))
+            nd = [l0, l1]
+            if "ppvb128" in ABL:    # timing only: one plain 16-byte read instead of two transposing ones
+                nd = [Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(V_RD + db)} offset:{off}", vrange(w, 4))]
+            if "ppnov" in ABL:      # timing only: no V operand reads
+                nd = []
             k += 1
             pr = S(sbuf, 0, 0, 0) + 4 * j
             o = OA + 16 * db
-            out.append({"kind": "mfma", "needs": [l0, l1],
+            out.append({"kind": "mfma", "needs": nd,
                         "text": f"v_mfma_f32_32x32x16_bf16 {areg(o, 16)}, {vreg(w, 4)}, {vreg(pr, 4)}, "
                                 f"{areg(o, 16)}",
                         "dst": [], "src": vrange(w, 4) + vrange(pr, 4)})
@@ -1199,7 +1318,7 @@ def operand_macros(prefix, bf16):
             f'[slack] "{{v{FIN + 2}}}"(slack)', f'[neginf] "{{v{FIN + 3}}}"(neginf)']
     ins += [f'[{n}] "s"({n})' for n in ("lim", "lds_k", "lds_v", "lds_m", "kstep", "vstep", "klo", "khi",
                                          "kn", "vlo", "vhi", "vn", "mlo", "mhi", "mn", "fl", "ntiles")]
-    clob = list(range(KWIN, MWIN + 8)) + ([] if bf16 else list(range(MSEL, MSEL + 8)))
+    clob = list(range(KWIN, MSEL)) + ([] if bf16 else list(range(MSEL, MSEL + 8)))   # the windows
     clob += [MLOG + h for h in range(NH)] + list(range(T, FIN))
     cl = [f'"v{r}"' for r in clob] + [f'"a{r}"' for r in range(NAGPR)]
     cl += [f'"s{r}"' for r in range(80, 98)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
