@@ -32,6 +32,7 @@ import os
 import shutil
 import subprocess
 import sys
+import time
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 COPY_MIB = 512
@@ -224,6 +225,85 @@ def stall_main(args, cfg) -> None:
                   body)
 
 
+POWER_LOADS = [("cfg2", ["--config", "cfg2"]), ("cfg3", ["--config", "cfg3"]), ("cfg4", ["--config", "cfg4"]),
+               ("cfg5", ["--config", "cfg5"]), ("mfma_random", ["--mfma", "random"]),
+               ("mfma_const", ["--mfma", "const"])]
+
+
+def smi_sample() -> tuple[float | None, list[float]]:
+    """Socket power (W) and the XCD graphics clocks (MHz) from amd-smi."""
+    res = subprocess.run(["timeout", "20", "amd-smi", "metric", "-p", "-c"], capture_output=True, text=True)
+    watts, clocks, in_gfx = None, [], False
+    for line in res.stdout.splitlines():
+        t = line.strip()
+        if t.startswith("SOCKET_POWER:"):
+            try:
+                watts = float(t.split()[1])
+            except (IndexError, ValueError):
+                pass
+        elif t.startswith("GFX_"):
+            in_gfx = True
+        elif t.endswith(":") and not t.startswith("GFX_"):
+            in_gfx = t.startswith("GFX")
+        elif in_gfx and t.startswith("CLK:"):
+            try:
+                clocks.append(float(t.split()[1]))
+            except (IndexError, ValueError):
+                pass
+            in_gfx = False
+    return watts, clocks
+
+
+def power_main(args) -> None:
+    """Steady-state socket power and XCD clocks: each workload runs back to
+    back for --loop-s seconds in its own process; amd-smi is sampled twice in
+    the second half. The MFMA probe with random and with constant operands
+    gives the matrix core's sustained rate at the power and clock it can hold."""
+    from custom_ops_amd.workloads import CONFIGS
+    env = dict(os.environ, PYTHONPATH=ROOT)
+    idle_w, idle_c = smi_sample()
+    body = [f"idle: socket {idle_w} W", "",
+            f"  {'workload':<12} {'rate':>22} {'socket_W':>9} {'xcd_clock_MHz(min/mean/max)':>30}"]
+    rates = {}
+    for name, extra in POWER_LOADS:
+        cmd = [sys.executable, "-m", "custom_ops_amd.prof_workload", *extra, "--loop-s", str(args.loop_s)]
+        print("[power]", " ".join(cmd), flush=True)
+        proc = subprocess.Popen(["timeout", "-s", "KILL", str(int(args.loop_s) + 90), *cmd], env=env,
+                                stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        time.sleep(args.loop_s * 0.55 + 3)
+        samples = [smi_sample()]
+        time.sleep(1.0)
+        samples.append(smi_sample())
+        out, _ = proc.communicate()
+        if proc.returncode != 0:
+            raise RuntimeError(f"{name} failed ({proc.returncode}):\n{out[-2000:]}")
+        last = [l for l in out.splitlines() if l.startswith("prof_workload")][-1]
+        watts = [w for w, _ in samples if w is not None]
+        clocks = [c for _, cs in samples for c in cs[:8]]
+        if name.startswith("cfg"):
+            us = float(last.split(",")[-1].split()[0])
+            tflops = CONFIGS[name].flops / (us * 1e-6) / 1e12
+            rate = f"{us:.1f} us = {tflops:.0f} TFLOP/s"
+        else:
+            tflops = float(last.split(",")[-1].split()[0])
+            rate = f"{tflops:.0f} TFLOP/s"
+        rates[name] = tflops
+        w = max(watts) if watts else float("nan")
+        cl = (f"{min(clocks):.0f}/{sum(clocks) / len(clocks):.0f}/{max(clocks):.0f}" if clocks else "n/a")
+        body.append(f"  {name:<12} {rate:>22} {w:>9.0f} {cl:>30}")
+    body += ["", "derived:",
+             f"  cfg2 / mfma_random                 {rates['cfg2'] / rates['mfma_random']:.3f}",
+             f"  mfma_random / 2500 TFLOP/s         {rates['mfma_random'] / 2500:.3f}",
+             f"  mfma_const / 2500 TFLOP/s          {rates['mfma_const'] / 2500:.3f}"]
+    write_summary(os.path.join(args.out, "power_clocks.txt"),
+                  "# socket power and XCD clocks under each workload (amd-smi, steady state)",
+                  [f"python -m custom_ops_amd.prof_collect --power --loop-s {args.loop_s}"]
+                  + ["python -m custom_ops_amd.prof_workload " + " ".join(e) + f" --loop-s {args.loop_s}"
+                     for _, e in POWER_LOADS]
+                  + ["amd-smi metric -p -c   (sampled twice in the second half of each run)"],
+                  body)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", default="cfg2")
@@ -232,6 +312,8 @@ def main() -> None:
     ap.add_argument("--hbm", action="store_true", help="cold HBM read ceiling instead")
     ap.add_argument("--stall", action="store_true", help="wave-state counters instead")
     ap.add_argument("--bench", action="store_true", help="kernel trace of bench.py's timed run instead")
+    ap.add_argument("--power", action="store_true", help="socket power and clocks per workload instead")
+    ap.add_argument("--loop-s", type=float, default=10.0, help="--power: seconds per workload")
     args = ap.parse_args()
     args.out = os.path.abspath(args.out)      # the passes run with cwd=/tmp
     os.makedirs(args.out, exist_ok=True)
@@ -242,6 +324,9 @@ def main() -> None:
         return
     if args.bench:
         bench_main(args)
+        return
+    if args.power:
+        power_main(args)
         return
     cfg = CONFIGS[args.config]
     if args.stall:
