@@ -939,7 +939,7 @@ PP_MBASE = 6 * PP_KST
 PP_LDS = PP_MBASE + 2 * PP_MST      # 160 KiB
 PP_KSLOTS = 6
 PP_VSLOTS = 6
-PP_KPRE = 4                          # K operands read in the V phase before
+PP_KPRE = next((int(a[4:]) for a in ABL if a.startswith("kpre")), 6)   # K operands read in the V phase before
 PP_DK = (0, 8, 32, 40)               # key offset of K DMA load i (16 rows on, π-permuted)
 
 
@@ -1008,6 +1008,9 @@ def pp_k_preread(kstage):
 # experiment: the P conversion and row sum of tile t in the M phase of tile
 # t+1 (slower: the M phase lengthens by more than the V phase shortens)
 P_IN_M = "ppinm" in ABL
+
+# experiment: a tile's DMA issued from the V phase after its M phase
+DMA_IN_V = "ppdmav" in ABL
 
 PP_MCHUNKS = [(0, 0), (1, 0), (0, 1), (1, 1)]   # (block b, chunk c), issue order
 
@@ -1089,9 +1092,10 @@ def pp_pv_mfmas(vstage, sbuf, p_here=False):
 
 
 def pp_dma_items(t_plus2_kstage, t_plus1_vstage, mstage, group_a, parts="kvm"):
-    """One M phase's DMA: group A all K(t+2) and V(t+1) loads of the workgroup
-    (4 each), every wave its own mask rows of tile t+2; parts selects K, V
-    and mask. Every load has its source offset in a register of its own
+    """One M phase's DMA: group A all K(t+2) loads of the workgroup, group B
+    all V(t+1) loads (4 each per wave; B's M phase runs one phase after A's,
+    and V(t+1) is first read by A's M(t+2), two phases on), every wave its own
+    mask rows of tile t+2; parts selects K, V and mask. Every load has its source offset in a register of its own
     (fixed per lane; the descriptor base moves one tile per batch), and its M0
     write is a separate item, so the phase scheduler puts an MFMA between the
     two instead of a wait state. Returns (items, VMEM count)."""
@@ -1110,13 +1114,14 @@ def pp_dma_items(t_plus2_kstage, t_plus1_vstage, mstage, group_a, parts="kvm"):
 
     # loads 2 and 3 of each tensor use its second descriptor (s68 K, s72 V,
     # s76 mask), whose base is 32 keys / 32 rows / 16 mask rows on
-    if group_a and "ppnokv" not in ABL:   # (ppnokv: timing only, no K/V DMA)
-        if "k" in parts:
+    kv_a = "ppkva" in ABL       # experiment: group A issues V as well
+    if "ppnokv" not in ABL:     # (ppnokv: timing only, no K/V DMA)
+        if "k" in parts and group_a:
             for i in range(4):
                 load(80 if i < 2 else 68, "lds_k", t_plus2_kstage * PP_KST + i * 4096, K_OFF + i % 2)
             adv(80, "%[kstep]")
             adv(68, "%[kstep]")
-        if "v" in parts:
+        if "v" in parts and group_a == kv_a:
             for i in range(4):
                 load(84 if i < 2 else 72, "lds_v", PP_VBASE + t_plus1_vstage * PP_KST + i * 4096,
                      V_OFF + i % 2)
@@ -1159,7 +1164,7 @@ def gen_pp(bf16: bool = True) -> str:
     st.ready.clear()
 
     # prologue: K(0), V(0), mask(0) into stage 0, K(1), mask(1) into stage 1
-    # (K/V by group A only), all landed before the common barrier
+    # (K by group A, V by group B), all landed before the common barrier
     st.emit("s_cmp_eq_u32 %[grp], 0")
     st.emit(f"s_cbranch_scc0 {L}_pb")
     pa = []
@@ -1171,7 +1176,7 @@ def gen_pp(bf16: bool = True) -> str:
     st.emit(f"{L}_pb:")
     pb = []
     for kst in (0, 1):
-        it, _ = pp_dma_items(0, 0, kst, False)
+        it, _ = pp_dma_items(0, 0, kst, False, parts="vm" if kst == 0 else "m")
         pb += it
     emit_groups(st, pb)
     st.emit(f"{L}_pj:")
@@ -1228,6 +1233,8 @@ def pp_group(group_a, L):
             if P_IN_M:
                 pv = pp_p_valus((t - 1) % 2)
         items, n = ([], 0) if last else pp_dma_items((t + 2) % 3, (t + 1) % 3, t % 2, group_a)
+        if DMA_IN_V:             # this tile's DMA goes out in the V phase after
+            items, n = [], 0
         if "ppnomf" in ABL:      # timing only: no MFMAs (the DMA still runs)
             mf = []
         Phase(st).run(mf, pv, items)
@@ -1240,7 +1247,7 @@ def pp_group(group_a, L):
             st.emit("s_barrier")
         return n
 
-    def v_phase(t, lab):
+    def v_phase(t, lab, last=False):
         vy = [tail_item(f"{lab}_t", t % 2, left=0)] + max_valus(t % 2)
         vy.append({"kind": "raw", "lines": rescale_lines(f"{lab}_r")})
         if P_IN_M:               # P stays fp32 until the next M phase
@@ -1254,6 +1261,9 @@ def pp_group(group_a, L):
         if "ppnomask" not in ABL:   # (ppnomask: timing only, no mask reads)
             vy += pp_mask_preread((t + 1) % 2)
         vy += [pp_k_preread((t + 1) % 3)]
+        if DMA_IN_V and not last:
+            dma, _ = pp_dma_items((t + 2) % 3, (t + 1) % 3, t % 2, group_a)
+            vy = interleave(vy, dma)
         stamp(2)
         Phase(st).run([], vy)
         stamp(3)
