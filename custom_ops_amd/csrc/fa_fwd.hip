@@ -51,7 +51,10 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <mutex>
+#include <random>
 #include <type_traits>
 
 #include "mi355_fa.h"
@@ -68,6 +71,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBN = 64;          // keys per KV tile
 constexpr int kMaxSplits = 64;
+constexpr int kFuseMaxSplits = 2;   // the fused split tail serves launches of at most this many splits
+constexpr int kCpolSc1 = 16;        // buffer cache policy: SC1 (device scope)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ── element traits ───────────────────────────────────────────────────────────
@@ -172,6 +177,13 @@ struct KParams {
   // scale·log2(e) and the rescale slack in score units, as float bits: kernel
   // arguments arrive in SGPRs, which the assembly loops take as scalar operands
   uint32_t c2_bits, slack_bits;
+  // Fused split tail (split launches with fuse set): every split counts itself
+  // in on its row block's ticket word (48-bit launch tag above a 16-bit
+  // count), and the last one combines the block; no combine launch follows.
+  unsigned long long* tickets;
+  unsigned long long tag;   // this launch's tag, below 2^48, never 0
+  int fuse;
+  uint32_t part_bytes, lse_bytes;   // sizes of o_part and lse_part (fuse: both below 2^31)
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -342,6 +354,14 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // which no other wave touches. l_run is this lane's partial row sum (the
 // lane 32 apart holds the rest), m_run the row's running max of
 // u = q·k + mask/scale.
+// The row block's ticket word (fused split tail): one per (batch, head group,
+// m-block), shared by that block's splits; ti as tile_index returns it.
+template <int BM>
+__device__ __forceinline__ int ticket_of(const KParams& p, const TileIdx& ti) {
+  const int ng = p.h / p.pack;
+  return (ti.b * ng + ti.h / p.pack) * p.num_m + ti.m0 / (BM / p.pack);
+}
+
 template <int D, bool BF16, bool SPLIT>
 __device__ __forceinline__ void write_rows(const KParams& p, const f32x16 (&oacc)[D / 32], float l_run,
                                            float m_run, int b, int h, int split, int qrow, uint8_t* stg,
@@ -386,15 +406,125 @@ __device__ __forceinline__ void write_rows(const KParams& p, const f32x16 (&oacc
     const int64_t bh = (int64_t)b * p.h + h;
     const int64_t slab = (int64_t)p.b * p.h * p.sq;
     const int64_t pbase = (int64_t)split * slab + bh * p.sq;
+    const float lse = (l == 0.f || l != l) ? -INFINITY
+                      : __builtin_fmaf(m_run, p.scale, __builtin_amdgcn_logf(l) * 0.69314718f);
+    if (p.fuse) {
+      // device-scope (sc1) stores: written through to where every XCD reads
+      // them, done once this wave's vmcnt drains (the fused tail's release)
+      const rsrc_t rp = make_rsrc(p.o_part, p.part_bytes), rl = make_rsrc(p.lse_part, p.lse_bytes);
 #pragma unroll
-    for (int k = 0; k < 32 / RPI; ++k) {
-      const int r = r0 + k * RPI;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
-      if (row0 + r < p.sq) *reinterpret_cast<u32x4*>(p.o_part + (pbase + row0 + r) * D + ch * 8) = v;
+      for (int k = 0; k < 32 / RPI; ++k) {
+        const int r = r0 + k * RPI;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
+        if (row0 + r < p.sq)
+          __builtin_amdgcn_raw_buffer_store_b128(v, rp, (uint32_t)(((pbase + row0 + r) * D + ch * 8) * 2), 0,
+                                                 kCpolSc1);
+      }
+      if (g == 0 && qrow < p.sq)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, lse), rl,
+                                              (uint32_t)((pbase + qrow) * 4), 0, kCpolSc1);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 32 / RPI; ++k) {
+        const int r = r0 + k * RPI;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * D * 2 + ((ch ^ (r & (CH - 1))) * 16));
+        if (row0 + r < p.sq) *reinterpret_cast<u32x4*>(p.o_part + (pbase + row0 + r) * D + ch * 8) = v;
+      }
+      if (g == 0 && qrow < p.sq) p.lse_part[pbase + qrow] = lse;
     }
-    if (g == 0 && qrow < p.sq)
-      p.lse_part[pbase + qrow] = (l == 0.f || l != l) ? -INFINITY
-                                 : __builtin_fmaf(m_run, p.scale, __builtin_amdgcn_logf(l) * 0.69314718f);
+  }
+}
+
+// Fused split tail, run by every thread of a split workgroup after its rows'
+// partials are stored (sc1). Once all of them have completed, one lane counts
+// the workgroup in on its row block's ticket; the split that completes the
+// count combines the block's rows from every split's partials (sc1 loads, so
+// no stale L2 line of this XCD is read), with the combine kernel's arithmetic.
+// Nothing waits on another workgroup. flag is one word of LDS no wave is using.
+// The row block is recomputed here from the workgroup id. (The compiled
+// kernel only: the assembly loops leave no registers for it.)
+template <int D, bool BF16, int BM, int NT>
+__device__ __forceinline__ void fused_tail(uint32_t* flag) {
+  typedef typename Elt<BF16>::v8 V8;
+  // The kernel's parameters (its only argument, at the start of the kernarg
+  // segment) are read here by scalar loads, not held in SGPRs from the
+  // kernel's entry across the tile loop: the pointer passes through an empty
+  // asm statement, so the loads cannot be hoisted.
+#if defined(__HIP_DEVICE_COMPILE__)
+  const KParams* kq = (const KParams*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(kq));
+#else
+  const KParams* kq = reinterpret_cast<const KParams*>(flag);   // host pass only: never runs
+#endif
+  const KParams& p = *kq;
+  if (!p.fuse) return;
+  const TileIdx tb = tile_index<BM>(p);
+  const int ticket = ticket_of<BM>(p, tb), b = tb.b, h0 = tb.h, m0 = tb.m0;
+  wait_vmcnt<0>();
+  wg_barrier();
+  if (threadIdx.x == 0) {
+    unsigned long long* w = p.tickets + ticket;
+    unsigned long long old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), nw;
+    do {
+      nw = ((old >> 16) == p.tag) ? old + 1 : ((p.tag << 16) | 1ull);
+    } while (!__hip_atomic_compare_exchange_weak(w, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT));
+    *flag = ((nw & 0xffffull) == (unsigned long long)p.num_splits) ? 1u : 0u;
+  }
+  wg_barrier();
+  if (*flag == 0u) return;
+  // rows of the block: head h0 + rr / (BM / pack), row m0 + rr % (BM / pack)
+  constexpr int kTPR = D / 8, kRPP = NT / kTPR, kPer = BM / kRPP;
+  constexpr int kS = kFuseMaxSplits;
+  const int S = p.num_splits;
+  const int tid = threadIdx.x, c8 = tid % kTPR, rp0 = tid / kTPR;
+  const int rows_h = BM / p.pack;
+  const int64_t slab = (int64_t)p.b * p.h * p.sq;
+  const rsrc_t rpart = make_rsrc(p.o_part, p.part_bytes), rlse = make_rsrc(p.lse_part, p.lse_bytes);
+  float lse[kPer][kS];
+  u32x4 raw[kPer][kS];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int rr = rp0 + k * kRPP;
+    const int h = h0 + rr / rows_h, m = m0 + rr % rows_h;
+    const int64_t row = ((int64_t)b * p.h + h) * p.sq + m;
+    const bool ok = m < p.sq;
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const bool in = ok && s < S;
+      lse[k][s] = in ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                           rlse, (uint32_t)((s * slab + row) * 4), 0, kCpolSc1))
+                     : -INFINITY;
+      raw[k][s] = __builtin_amdgcn_raw_buffer_load_b128(
+          rpart, in ? (uint32_t)(((s * slab + row) * D + c8 * 8) * 2) : 0x80000000u, 0, kCpolSc1);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int rr = rp0 + k * kRPP;
+    const int h = h0 + rr / rows_h, m = m0 + rr % rows_h;
+    if (m >= p.sq) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kS; ++s) mx = fmaxf(mx, lse[k][s]);
+    const float mxc = (mx == -INFINITY) ? 0.f : mx;
+    float w[kS], sum = 0.f;
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      w[s] = __builtin_amdgcn_exp2f((lse[k][s] - mxc) * kLog2e);
+      sum += w[s];
+    }
+    const float inv = (sum > 0.f) ? 1.f / sum : 0.f;
+#pragma unroll
+    for (int s = 0; s < kS; ++s) w[s] *= inv;
+    f32x8 acc = {};
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const u32x4 x = (w[s] != 0.f) ? raw[k][s] : u32x4{0u, 0u, 0u, 0u};
+      acc += w[s] * __builtin_convertvector(bitcast<V8>(x), f32x8);
+    }
+    uint16_t* dst = p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs + (int64_t)m * p.o_rs + c8 * 8;
+    *reinterpret_cast<u32x4*>(dst) = bitcast<u32x4>(__builtin_convertvector(acc, V8));
   }
 }
 
@@ -864,6 +994,7 @@ void fa_fwd_kernel(const KParams p) {
   uint8_t* stg = (a.wave < 4 ? reinterpret_cast<uint8_t*>(&sK[0][0]) : reinterpret_cast<uint8_t*>(&sV[0][0]))
                  + (a.wave & 3) * 32 * D * 2;
   a.epilogue(ti.b, ti.h, ti.split, qrow, stg);
+  if constexpr (SPLIT) fused_tail<D, BF16, G::kBM, G::kThreads>(reinterpret_cast<uint32_t*>(&sK[0][0]));
 }
 
 // ── software-pipelined tile loop in generated assembly (d = 128) ─────────────
@@ -1370,11 +1501,21 @@ static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int 
   return best;
 }
 
+// MI355_FA_FUSE=0 keeps the combine launch for every split plan (A/B runs)
+static bool fuse_enabled() {
+  static const bool f = [] {
+    const char* e = getenv("MI355_FA_FUSE");
+    return !(e && e[0] == '0');
+  }();
+  return f;
+}
+
 struct Plan {
   int waves, block_m, num_m, num_n, splits, n_per_split;
   int pack;   // q-heads per workgroup; block_m / pack rows of each
   int head_major;
-  size_t o_part_bytes, lse_bytes, ws_bytes;
+  size_t o_part_bytes, lse_bytes, ticket_bytes, ws_bytes;
+  int fuse;   // split tail fused into the main kernel (no combine launch)
 };
 
 // Tile plan: the workgroup size (4 or 8 waves) and split count with the
@@ -1488,8 +1629,16 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
     const size_t rows = (size_t)s * p->b * p->h * p->seqlen_q;
     pl.o_part_bytes = (rows * p->d * sizeof(uint16_t) + 255) & ~(size_t)255;
     pl.lse_bytes = (rows * sizeof(float) + 255) & ~(size_t)255;
+    // one ticket word per row block (batch, head group, m-block)
+    const size_t tickets = (size_t)p->b * (p->h / pl.pack) * pl.num_m;
+    pl.ticket_bytes = (tickets * 8 + 255) & ~(size_t)255;
+    // fused tail: two splits (the last one's combine reads two partials per
+    // row); more splits keep the combine launch, whose work spreads over the
+    // whole chip instead of falling on each row block's last split
+    pl.fuse = s <= kFuseMaxSplits && pl.o_part_bytes < (1ull << 31) && pl.lse_bytes < (1ull << 31) &&
+              fuse_enabled();
   }
-  pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes;
+  pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
   return pl;
 }
 
@@ -1556,6 +1705,25 @@ static hipError_t launch_main(const KParams& kp, hipStream_t st) {
 // The generated-loop kernel serves the 8-wave plans at d = 128 with 16-byte
 // aligned mask rows. MI355_FA_ASM selects its form: 1 (default) = 8 waves of
 // 32 rows, 2 = 4 waves of 64 rows, 0 = the compiled 8-wave kernel instead.
+// A 48-bit launch tag, never 0, distinct for every launch of the process
+// (splitmix64 of a per-process random seed plus a launch counter): a ticket
+// word left by an earlier launch in reused workspace memory carries another
+// tag, so the first split of this launch restarts its count.
+static unsigned long long next_launch_tag() {
+  static std::atomic<unsigned long long> ctr{0};
+  static const unsigned long long seed = [] {
+    std::random_device rd;
+    return ((unsigned long long)rd() << 32) ^ rd() ^
+           (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count();
+  }();
+  unsigned long long z = seed + 0x9e3779b97f4a7c15ull * (ctr.fetch_add(1) + 1);
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  z ^= z >> 31;
+  z &= (1ull << 48) - 1;
+  return z ? z : 1ull;
+}
+
 static int asm_form() {
   static const int f = [] {
     const char* e = getenv("MI355_FA_ASM");
@@ -1566,12 +1734,19 @@ static int asm_form() {
   return f;
 }
 
+// Whether a launch runs one of the generated-assembly loops (d = 128, 8-wave
+// plans, 16-byte aligned mask rows) rather than the compiled kernel.
+template <int D, bool BF16>
+static bool runs_asm_loop(const KParams& kp, const Plan& pl) {
+  // bf16 adds the mask on the matrix core, which needs bf16(1/scale) > 1.0078
+  // (-max_bf16 · (1/scale) must overflow to -inf): scale < 0.99
+  return D == 128 && pl.waves == 8 && kp.mask_direct && asm_form() && (!BF16 || kp.scale < 0.99f);
+}
+
 template <int D, bool BF16, bool SPLIT>
 static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t st) {
   if constexpr (D == 128) {
-    // bf16 adds the mask on the matrix core, which needs bf16(1/scale) > 1.0078
-    // (-max_bf16 · (1/scale) must overflow to -inf): scale < 0.99
-    if (pl.waves == 8 && kp.mask_direct && asm_form() && (!BF16 || kp.scale < 0.99f)) {
+    if (runs_asm_loop<D, BF16>(kp, pl)) {
       if (asm_form() == 3 && BF16)
         hipLaunchKernelGGL((fa_fwd_kernel_pp<SPLIT>), dim3(kp.total), dim3(512), 0, st, kp);
       else if (asm_form() == 2)
@@ -1588,8 +1763,12 @@ static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t 
 template <int D, bool BF16>
 static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, hipStream_t st) {
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
-  hipError_t e = launch_variant<D, BF16, true>(kp, pl, st);
-  if (e != hipSuccess) return e;
+  // the fused tail is in the compiled kernel only (the assembly loops keep no
+  // registers for it): their split launches keep the combine launch
+  KParams kf = kp;
+  kf.fuse = kp.fuse && !runs_asm_loop<D, BF16>(kp, pl);
+  hipError_t e = launch_variant<D, BF16, true>(kf, pl, st);
+  if (e != hipSuccess || kf.fuse) return e;
   // 256-thread workgroups while they still number >= 1024, else one wave each.
   constexpr int kRows256 = 256 / (D / 8), kRows64 = 64 / (D / 8);
   if ((cp.rows + kRows256 - 1) / kRows256 >= 1024) {
@@ -1698,6 +1877,11 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   if (split) {
     kp.o_part = (uint16_t*)p->workspace;
     kp.lse_part = (float*)((char*)p->workspace + pl.o_part_bytes);
+    kp.tickets = (unsigned long long*)((char*)p->workspace + pl.o_part_bytes + pl.lse_bytes);
+    kp.fuse = pl.fuse;
+    kp.tag = pl.fuse ? next_launch_tag() : 0ull;
+    kp.part_bytes = (uint32_t)std::min<size_t>(pl.o_part_bytes, 0xffffffffu);
+    kp.lse_bytes = (uint32_t)std::min<size_t>(pl.lse_bytes, 0xffffffffu);
     cp.o_part = kp.o_part;
     cp.lse_part = kp.lse_part;
     cp.o = kp.o;

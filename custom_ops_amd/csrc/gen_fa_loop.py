@@ -202,8 +202,11 @@ class Phase:
     """
     MAXQ = 12
 
-    def __init__(self, st):
+    def __init__(self, st, maxq=None):
         self.st = st
+        if maxq:
+            assert maxq <= 15, "lgkmcnt tracks at most 15 LDS reads"
+            self.MAXQ = maxq
 
     def run(self, mfmas, valus, others=(), valu_lead=0, exact=False, others_span=None):
         """exact: every VALU item carries the MFMA slot it follows (min_mfma,
@@ -937,8 +940,9 @@ PP_MST = 32768
 PP_VBASE = 3 * PP_KST
 PP_MBASE = 6 * PP_KST
 PP_LDS = PP_MBASE + 2 * PP_MST      # 160 KiB
-PP_KSLOTS = 6
-PP_VSLOTS = 6
+PP_KSLOTS = next((int(a[2:]) for a in ABL if a.startswith("ks")), 6)   # K operand window slots
+PP_VSLOTS = next((int(a[2:]) for a in ABL if a.startswith("vs")), 6)   # V (and mask) window slots
+PP_MAXQ = next((int(a[1:]) for a in ABL if a[:1] == "q" and a[1:].isdigit()), 12)   # LDS reads in flight
 PP_KPRE = next((int(a[4:]) for a in ABL if a.startswith("kpre")), 6)   # K operands read in the V phase before
 PP_DK = (0, 8, 32, 40)               # key offset of K DMA load i (16 rows on, π-permuted)
 
@@ -1221,7 +1225,7 @@ def pp_group(group_a, L):
     if not group_a:
         st.emit("s_barrier")
     # operands of M_0: mask(0) clamped, K(0)'s first operands
-    Phase(st).run([], pp_mask_preread(0) + [pp_k_preread(0)])
+    Phase(st, PP_MAXQ).run([], pp_mask_preread(0) + [pp_k_preread(0)])
 
     def m_phase(t, first, last, prev_batch):
         """M_t; t is the tile index mod 6 (stages and buffers)."""
@@ -1237,7 +1241,7 @@ def pp_group(group_a, L):
             items, n = [], 0
         if "ppnomf" in ABL:      # timing only: no MFMAs (the DMA still runs)
             mf = []
-        Phase(st).run(mf, pv, items)
+        Phase(st, PP_MAXQ).run(mf, pv, items)
         # the batch of the previous M phase has landed (LDS DMA: visible to
         # the other waves after the barrier)
         if prev_batch is not None:
@@ -1265,7 +1269,7 @@ def pp_group(group_a, L):
             dma, _ = pp_dma_items((t + 2) % 3, (t + 1) % 3, t % 2, group_a)
             vy = interleave(vy, dma)
         stamp(2)
-        Phase(st).run([], vy)
+        Phase(st, PP_MAXQ).run([], vy)
         stamp(3)
         st.emit("s_barrier")
 

@@ -77,7 +77,8 @@ typedef struct mi355_fa_params {
 
   /* Split-KV: 0 = let the library plan it; >= 1 forces that many splits. */
   int32_t num_splits;
-  /* Device workspace for split-KV partials (may be NULL when no split is planned). */
+  /* Device workspace for split-KV partials and the fused split tail's ticket
+   * words (may be NULL when no split is planned; its contents need no clearing). */
   void* workspace;
   size_t workspace_bytes;
 } mi355_fa_params;
