@@ -444,22 +444,25 @@ __device__ __forceinline__ void write_rows(const KParams& p, const f32x16 (&oacc
 // The row block is recomputed here from the workgroup id. (The compiled
 // kernel only: the assembly loops leave no registers for it.)
 template <int D, bool BF16, int BM, int NT>
-__device__ __forceinline__ void fused_tail(uint32_t* flag) {
+__device__ __forceinline__ void fused_tail(float* tl, const uint8_t* stg_lo, const uint8_t* stg_hi) {
   typedef typename Elt<BF16>::v8 V8;
+  constexpr int kS = kFuseMaxSplits;
+  static_assert(NT == kS * BM, "one thread per (row, split) LSE");
+  uint32_t* flag = reinterpret_cast<uint32_t*>(tl + kS * BM);
   // The kernel's parameters (its only argument, at the start of the kernarg
-  // segment) are read here by scalar loads, not held in SGPRs from the
-  // kernel's entry across the tile loop: the pointer passes through an empty
-  // asm statement, so the loads cannot be hoisted.
+  // segment) are read here, not held in SGPRs from the kernel's entry across
+  // the tile loop: the pointer passes through an empty asm statement, so the
+  // loads cannot be hoisted.
 #if defined(__HIP_DEVICE_COMPILE__)
   const KParams* kq = (const KParams*)__builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(kq));
 #else
-  const KParams* kq = reinterpret_cast<const KParams*>(flag);   // host pass only: never runs
+  const KParams* kq = reinterpret_cast<const KParams*>(tl);   // host pass only: never runs
 #endif
   const KParams& p = *kq;
   if (!p.fuse) return;
   const TileIdx tb = tile_index<BM>(p);
-  const int ticket = ticket_of<BM>(p, tb), b = tb.b, h0 = tb.h, m0 = tb.m0;
+  const int ticket = ticket_of<BM>(p, tb), b = tb.b, h0 = tb.h, m0 = tb.m0, own = tb.split;
   wait_vmcnt<0>();
   wg_barrier();
   if (threadIdx.x == 0) {
@@ -473,55 +476,74 @@ __device__ __forceinline__ void fused_tail(uint32_t* flag) {
   }
   wg_barrier();
   if (*flag == 0u) return;
-  // rows of the block: head h0 + rr / (BM / pack), row m0 + rr % (BM / pack)
-  constexpr int kTPR = D / 8, kRPP = NT / kTPR, kPer = BM / kRPP;
-  constexpr int kS = kFuseMaxSplits;
+  // Block row rr: head h0 + rr / (BM / pack), row m0 + rr % (BM / pack). Its
+  // own split's partial is still in the LDS staging of the wave that wrote it
+  // (wave j + pack·(m / 32) for head slot j and block-local row m, 32 rows of
+  // D elements each, 16-byte units XOR-swizzled by row); the other split's
+  // comes by sc1 loads. Weights as in the combine kernel.
+  constexpr int CH = D / 8, kTPR = CH, kRPP = NT / kTPR, kPer = BM / kRPP;
   const int S = p.num_splits;
   const int tid = threadIdx.x, c8 = tid % kTPR, rp0 = tid / kTPR;
   const int rows_h = BM / p.pack;
   const int64_t slab = (int64_t)p.b * p.h * p.sq;
   const rsrc_t rpart = make_rsrc(p.o_part, p.part_bytes), rlse = make_rsrc(p.lse_part, p.lse_bytes);
-  float lse[kPer][kS];
+  auto grow = [&](int rr, int& h, int& m) {
+    h = h0 + rr / rows_h;
+    m = m0 + rr % rows_h;
+    return ((int64_t)b * p.h + h) * p.sq + m;
+  };
   u32x4 raw[kPer][kS];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const int rr = rp0 + k * kRPP;
-    const int h = h0 + rr / rows_h, m = m0 + rr % rows_h;
-    const int64_t row = ((int64_t)b * p.h + h) * p.sq + m;
-    const bool ok = m < p.sq;
+    int h, m;
+    const int64_t row = grow(rp0 + k * kRPP, h, m);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      const bool in = ok && s < S;
-      lse[k][s] = in ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                           rlse, (uint32_t)((s * slab + row) * 4), 0, kCpolSc1))
-                     : -INFINITY;
+      const bool in = m < p.sq && s < S && s != own;
       raw[k][s] = __builtin_amdgcn_raw_buffer_load_b128(
           rpart, in ? (uint32_t)(((s * slab + row) * D + c8 * 8) * 2) : 0x80000000u, 0, kCpolSc1);
     }
   }
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int rr = rp0 + k * kRPP;
-    const int h = h0 + rr / rows_h, m = m0 + rr % rows_h;
-    if (m >= p.sq) continue;
+  {
+    const int rr = tid % BM, s = tid / BM;
+    int h, m;
+    const int64_t row = grow(rr, h, m);
+    tl[s * BM + rr] = (m < p.sq && s < S) ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                rlse, (uint32_t)((s * slab + row) * 4), 0, kCpolSc1))
+                                          : -INFINITY;
+  }
+  __syncthreads();
+  if (tid < BM) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < kS; ++s) mx = fmaxf(mx, lse[k][s]);
+    for (int s = 0; s < kS; ++s) mx = fmaxf(mx, tl[s * BM + tid]);
     const float mxc = (mx == -INFINITY) ? 0.f : mx;
     float w[kS], sum = 0.f;
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      w[s] = __builtin_amdgcn_exp2f((lse[k][s] - mxc) * kLog2e);
+      w[s] = __builtin_amdgcn_exp2f((tl[s * BM + tid] - mxc) * kLog2e);
       sum += w[s];
     }
     const float inv = (sum > 0.f) ? 1.f / sum : 0.f;
 #pragma unroll
-    for (int s = 0; s < kS; ++s) w[s] *= inv;
+    for (int s = 0; s < kS; ++s) tl[s * BM + tid] = w[s] * inv;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int rr = rp0 + k * kRPP;
+    int h, m;
+    grow(rr, h, m);
+    if (m >= p.sq) continue;
+    const int j = rr / rows_h, ml = rr % rows_h, wv = j + p.pack * (ml / 32), r32 = ml % 32;
+    const uint8_t* st = (wv < 4 ? stg_lo : stg_hi) + (wv & 3) * 32 * D * 2;
+    const u32x4 mine = *reinterpret_cast<const u32x4*>(st + r32 * D * 2 + ((c8 ^ (r32 & (CH - 1))) * 16));
     f32x8 acc = {};
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      const u32x4 x = (w[s] != 0.f) ? raw[k][s] : u32x4{0u, 0u, 0u, 0u};
-      acc += w[s] * __builtin_convertvector(bitcast<V8>(x), f32x8);
+      const float ws = tl[s * BM + rr];
+      const u32x4 x = (ws != 0.f) ? (s == own ? mine : raw[k][s]) : u32x4{0u, 0u, 0u, 0u};
+      acc += ws * __builtin_convertvector(bitcast<V8>(x), f32x8);
     }
     uint16_t* dst = p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs + (int64_t)m * p.o_rs + c8 * 8;
     *reinterpret_cast<u32x4*>(dst) = bitcast<u32x4>(__builtin_convertvector(acc, V8));
@@ -886,6 +908,8 @@ void fa_fwd_kernel(const KParams p) {
   __shared__ __align__(16) uint16_t sK[NST][G::kKElems];
   __shared__ __align__(16) uint16_t sV[NST][G::kVElems];
   __shared__ __align__(16) uint16_t sM[A::MREG ? 8 : G::kMElems];
+  // fused split tail: per (split, row) LSEs then weights, and the ticket flag
+  __shared__ __align__(16) float sTail[SPLIT ? kFuseMaxSplits * G::kBM + 4 : 4];
 
   TileIdx ti = tile_index<G::kBM>(p);
   place_wave(ti, p, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), 32);
@@ -994,7 +1018,9 @@ void fa_fwd_kernel(const KParams p) {
   uint8_t* stg = (a.wave < 4 ? reinterpret_cast<uint8_t*>(&sK[0][0]) : reinterpret_cast<uint8_t*>(&sV[0][0]))
                  + (a.wave & 3) * 32 * D * 2;
   a.epilogue(ti.b, ti.h, ti.split, qrow, stg);
-  if constexpr (SPLIT) fused_tail<D, BF16, G::kBM, G::kThreads>(reinterpret_cast<uint32_t*>(&sK[0][0]));
+  if constexpr (SPLIT)
+    fused_tail<D, BF16, G::kBM, G::kThreads>(sTail, reinterpret_cast<const uint8_t*>(&sK[0][0]),
+                                             reinterpret_cast<const uint8_t*>(&sV[0][0]));
 }
 
 // ── software-pipelined tile loop in generated assembly (d = 128) ─────────────
