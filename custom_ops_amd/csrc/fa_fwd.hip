@@ -184,6 +184,7 @@ struct KParams {
   unsigned long long tag;   // this launch's tag, below 2^48, never 0
   int fuse;
   uint32_t part_bytes, lse_bytes;   // sizes of o_part and lse_part (fuse: both below 2^31)
+  int live;   // narrow each workgroup's key range to its live tiles
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -312,6 +313,167 @@ __device__ __forceinline__ TileIdx tile_index(const KParams& p) {
 __device__ __forceinline__ void place_wave(TileIdx& ti, const KParams& p, int wave, int rows) {
   ti.h += wave % p.pack;
   ti.m0 += (wave / p.pack - wave) * rows;
+}
+
+// Live key range of a workgroup. A KV tile in which every mask entry of the
+// workgroup's rows is -inf adds nothing to any of them (their scores there are
+// all -inf: P = 0, and O, l and the running max are unchanged), so only the
+// tiles from the first to the last one that holds a visible entry need to run,
+// and the splits can share that range evenly instead of the whole key axis (an
+// empty share runs no tile and leaves O = 0, LSE = -inf).
+//  * live_probe: one 16-byte load per thread of the first and of the last tile
+//    of the key axis (the first NT/8 rows of the workgroup), issued before the
+//    kernel's own prologue loads so that one memory wait covers both.
+//  * narrow_to_live: if the probe saw a visible entry at both ends (a dense
+//    mask) the range is the whole axis and the nominal split ranges stand: the
+//    cost is one OR over the workgroup. Otherwise the workgroup reads its rows'
+//    mask from both ends, a window of U whole tiles per end and step (J
+//    16-byte loads per thread and end per round, enough rounds to cover one
+//    tile), ORs the per-tile verdicts over the workgroup and stops on each side
+//    at the first tile with a visible entry: a sliding-window or causal mask
+//    reads its dead edges once. Returns whether the range moved.
+// Only entries that are exactly -inf count as blocked; columns >= Sk and rows
+// >= Sq are ignored. A chunk read partly past the end of the buffer reads 0
+// there, i.e. visible: that can only widen the range. Masks whose rows are not
+// 16-byte aligned are read with the same (unaligned) 16-byte loads the
+// compiled kernel's register mask path uses.
+// U >= 1 (kRounds rounds cover a tile of BMAX >= rows rows), so every step
+// either finds an end or moves it by at least one tile: the loop ends within
+// num_n steps, uniformly over the workgroup (every wave reads the same words).
+// Both functions read the parameters through the kernarg pointer passed
+// through an empty asm statement: the compiler then cannot keep them in SGPRs
+// across the tile loop (the assembly loops leave no registers to spill to).
+// `red` is 4·waves words of LDS that no DMA touches until the final barrier
+// (two sets, used alternately: a set is rewritten two steps after it was read,
+// past the next barrier).
+__device__ __forceinline__ const KParams& kernarg_params(const KParams& pk) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const KParams* kq = (const KParams*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(kq));
+  return *kq;
+#else
+  return pk;   // host pass only: never runs
+#endif
+}
+
+// whether the 8 entries of a chunk starting at column c0 hold a visible one
+template <bool BF16>
+__device__ __forceinline__ bool live8(u32x4 v, int c0, int sk) {
+  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u;
+  const int nv = sk - c0;
+  bool any = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t x = (v[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+    any |= (e < nv) && (x != kNeg);
+  }
+  return any;
+}
+
+// OR over the workgroup: within each 16-lane row by DPP, over the wave's four
+// rows by readlane, then one word per wave in LDS (set `set` of two), read by
+// every thread after a barrier
+template <int NT>
+__device__ __forceinline__ void wg_or2(uint32_t& a, uint32_t& b, uint32_t* red, int set) {
+  constexpr int kW = NT / 64;
+  auto row_or = [](uint32_t x) {
+    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);    // quad_perm 1,0,3,2
+    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);    // quad_perm 2,3,0,1
+    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x124, 0xF, 0xF, false);   // row_ror 4
+    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, false);   // row_ror 8
+    return __builtin_amdgcn_readlane(x, 0) | __builtin_amdgcn_readlane(x, 16) |
+           __builtin_amdgcn_readlane(x, 32) | __builtin_amdgcn_readlane(x, 48);
+  };
+  const uint32_t wa = row_or(a), wb = row_or(b);
+  const int tid = threadIdx.x;
+  uint32_t* w = red + 2 * kW * set;
+  w[tid >> 6] = wa;
+  w[kW + (tid >> 6)] = wb;
+  __syncthreads();
+  uint32_t ra = 0u, rb = 0u;
+#pragma unroll
+  for (int i = 0; i < kW; ++i) { ra |= w[i]; rb |= w[kW + i]; }
+  a = __builtin_amdgcn_readfirstlane(ra);
+  b = __builtin_amdgcn_readfirstlane(rb);
+}
+
+struct LiveProbe { u32x4 l, r; };
+
+template <int NT>
+__device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams& pk) {
+  const KParams& p = kernarg_params(pk);
+  LiveProbe pr{};
+  if (!p.live) return pr;
+  const rsrc_t rm = make_rsrc(p.mask + (int64_t)ti.b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+  const int tid = threadIdx.x;
+  const uint32_t rowoff = (uint32_t)(ti.m0 + (tid >> 3)) * (uint32_t)p.m_rs + (uint32_t)(tid & 7) * 8u;
+  pr.l = bload16(rm, rowoff * 2u);
+  pr.r = bload16(rm, (rowoff + (uint32_t)(p.num_n - 1) * kBN) * 2u);
+  return pr;
+}
+
+template <bool BF16, int NT, int BMAX, int J>
+__device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, int rows, const LiveProbe& pr,
+                                               uint32_t* red) {
+  const KParams& p = kernarg_params(pk);
+  if (!p.live) return false;
+  const int nr = min(rows, p.sq - ti.m0);
+  if (nr <= 0) return false;
+  const int tid = threadIdx.x;
+  const int nn = p.num_n;
+  // the probe's verdict: tile 0 / tile nn - 1 live in the chunks it read
+  uint32_t lb = (tid < nr * 8 && live8<BF16>(pr.l, (tid & 7) * 8, p.sk)) ? 1u : 0u;
+  uint32_t rb = (tid < nr * 8 && live8<BF16>(pr.r, (nn - 1) * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
+  wg_or2<NT>(lb, rb, red, 1);
+  if (lb && rb) {                          // whole axis live: the nominal ranges stand
+    __syncthreads();                       // every wave has read `red` before any DMA lands
+    return false;
+  }
+  int lo = lb ? 0 : -1, hi = rb ? nn - 1 : -1;
+  constexpr int kRounds = (8 * BMAX + J * NT - 1) / (J * NT);   // rounds that cover one whole tile
+  const int cpt = nr * 8;                  // 16-byte chunks per tile of these rows
+  int U = (kRounds * J * NT) / cpt;        // tiles per window: 1 .. 32
+  U = U > 32 ? 32 : U;
+  const rsrc_t rm = make_rsrc(p.mask + (int64_t)ti.b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+  int L = 0, R = nn - 1;
+  for (int step = 0; lo < 0 || hi < 0; ++step) {
+    if (L > R) break;                      // every tile scanned and dead
+    const int ul = lo < 0 ? min(U, R - L + 1) : 0;
+    const int ur = hi < 0 ? min(U, R - L + 1) : 0;
+    uint32_t lbits = 0u, rbits = 0u;
+#pragma unroll
+    for (int rd = 0; rd < kRounds; ++rd) {
+      // branch-free: a chunk outside the window loads tile L (in range) and
+      // is ignored
+      u32x4 vl[J], vr[J];
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int c = (rd * J + j) * NT + tid, t = c / cpt, rem = c - t * cpt;
+        const uint32_t rowoff = (uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u;
+        vl[j] = bload16(rm, (rowoff + (uint32_t)(t < ul ? L + t : L) * kBN) * 2u);
+        vr[j] = bload16(rm, (rowoff + (uint32_t)(t < ur ? R - t : L) * kBN) * 2u);
+      }
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int c = (rd * J + j) * NT + tid, t = c / cpt, rem = c - t * cpt;
+        const int c0 = (rem & 7) * 8;
+        const uint32_t bit = 1u << (t & 31);
+        lbits |= (t < ul && live8<BF16>(vl[j], (L + t) * kBN + c0, p.sk)) ? bit : 0u;
+        rbits |= (t < ur && live8<BF16>(vr[j], (R - t) * kBN + c0, p.sk)) ? bit : 0u;
+      }
+    }
+    wg_or2<NT>(lbits, rbits, red, step & 1);
+    if (lo < 0) { if (lbits) lo = L + __builtin_ctz(lbits); else L += ul; }
+    if (hi < 0) { if (rbits) hi = R - __builtin_ctz(rbits); else R -= ur; }
+  }
+  __syncthreads();                         // every wave has read `red` before any DMA lands
+  // no visible entry in these rows: an empty range (lo = 0, hi = -1)
+  if (lo < 0) { lo = 0; hi = -1; }
+  const int per = (hi - lo + 1 + p.num_splits - 1) / p.num_splits;
+  const int nb = min(lo + ti.split * per, hi + 1);
+  ti.nb = nb;
+  ti.ne = min(nb + per, hi + 1);
+  return true;
 }
 
 // ── main kernel: 32 query rows per wave, WAVES = 4 or 8 waves ─────────────────
@@ -912,10 +1074,12 @@ void fa_fwd_kernel(const KParams p) {
   __shared__ __align__(16) float sTail[SPLIT ? kFuseMaxSplits * G::kBM + 4 : 4];
 
   TileIdx ti = tile_index<G::kBM>(p);
+  const TileIdx tg = ti;   // the workgroup's first head and row
+  const LiveProbe lp = live_probe<G::kThreads>(tg, p);
   place_wave(ti, p, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), 32);
   A a(p);
   a.init(ti);
-  const int nb = ti.nb, ne = ti.ne;
+  int nb = ti.nb, ne = ti.ne;
   const rsrc_t rq = make_rsrc(p.q + (int64_t)ti.b * p.q_bs + (int64_t)ti.h * p.q_hs,
                               (uint32_t)p.sq * p.q_rs * 2u);
   const int qrow = ti.m0 + a.wave * 32 + a.l32;
@@ -929,17 +1093,33 @@ void fa_fwd_kernel(const KParams p) {
       for (int st = 0; st < NST; ++st) reinterpret_cast<u32x4*>(sV[st])[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
   }
-  const int cnt = ne - nb;
-  if (cnt > 0) a.issue_m(nb, sM);
+  int cnt = ne - nb;
+  auto first_tiles = [&]() {
+    if (cnt > 0) a.issue_m(nb, sM);
 #pragma unroll
-  for (int j = 0; j < NST - 1; ++j) {
-    if (j < cnt) {
-      a.issue_k(nb + j, sK[j]);
-      a.issue_v(nb + j, sV[j]);
+    for (int j = 0; j < NST - 1; ++j) {
+      if (j < cnt) {
+        a.issue_k(nb + j, sK[j]);
+        a.issue_v(nb + j, sV[j]);
+      }
+    }
+  };
+  first_tiles();
+  a.load_q(qrow, rq);
+  wait_vmcnt<0>();   // Q, the first tiles and the live probe, on every path into the loop
+  {
+    // the last K stage is not loaded before the loop's first barrier
+    TileIdx tn = tg;
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8>(tn, p, G::kBM / p.pack, lp,
+                                                       reinterpret_cast<uint32_t*>(&sK[NST - 1][0]))) {
+      // the range moved: the first tiles again, for its first tile
+      nb = tn.nb;
+      ne = tn.ne;
+      cnt = ne - nb;
+      first_tiles();
+      wait_vmcnt<0>();
     }
   }
-  a.load_q(qrow, rq);
-  wait_vmcnt<0>();   // Q and the first tiles, on every path into the loop
   if (cnt > 0) {
     a.commit_m(sM);
     a.mask_init(sM);
@@ -1065,6 +1245,12 @@ void fa_fwd_kernel_asm(const KParams p) {
   constexpr int ROWS = 32 * NH;                    // query rows per wave
   __shared__ __align__(16) uint8_t smem[kAsmLds];
   TileIdx ti = tile_index<256>(p);
+  {
+    // before the set-up below: its values would be live across the scan, and
+    // the registers the scan needs on top of them would spill
+    const LiveProbe lp = live_probe<64 * WAVES>(ti, p);
+    narrow_to_live<BF16, 64 * WAVES, 256, 4>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kAsmMBase));
+  }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   place_wave(ti, p, wave, ROWS);
@@ -1075,8 +1261,6 @@ void fa_fwd_kernel_asm(const KParams p) {
   const uint16_t* mbase = p.mask + (int64_t)ti.b * p.m_bs;
   const uint32_t kbytes = (uint32_t)p.sk * p.k_rs * 2u, vbytes = (uint32_t)p.sk * p.v_rs * 2u;
   const uint32_t mbytes = (uint32_t)p.msq * p.m_rs * 2u;
-  const int nb = ti.nb, ne = ti.ne;
-  const int cnt = ne - nb;
 
   // DMA sources: K rows permuted within 32-key blocks (a lane of the score
   // tile then owns 16 consecutive keys), V in key order, this wave's mask rows
@@ -1151,6 +1335,8 @@ void fa_fwd_kernel_asm(const KParams p) {
   }
   wait_vmcnt<0>();
   __syncthreads();
+  const int nb = ti.nb, ne = ti.ne;
+  const int cnt = ne - nb;
 
   const uint32_t ksh = (uint32_t)nb * kBN * (uint32_t)p.k_rs * 2u;
   const uint32_t vsh = (uint32_t)nb * kBN * (uint32_t)p.v_rs * 2u;
@@ -1227,6 +1413,12 @@ void fa_fwd_kernel_pp(const KParams p) {
   constexpr int UPR = D / 8;
   __shared__ __align__(16) uint8_t smem[kPpLds];
   TileIdx ti = tile_index<256>(p);
+  {
+    // before the set-up below: its values would be live across the scan, and
+    // the SGPRs the scan needs on top of them would spill
+    const LiveProbe lp = live_probe<512>(ti, p);
+    narrow_to_live<true, 512, 256, 4>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kPpMBase));
+  }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   place_wave(ti, p, wave, 32);
@@ -1236,7 +1428,6 @@ void fa_fwd_kernel_pp(const KParams p) {
   const uint16_t* mbase = p.mask + (int64_t)ti.b * p.m_bs;
   const uint32_t kbytes = (uint32_t)p.sk * p.k_rs * 2u, vbytes = (uint32_t)p.sk * p.v_rs * 2u;
   const uint32_t mbytes = (uint32_t)p.msq * p.m_rs * 2u;
-  const int nb = ti.nb, ne = ti.ne, cnt = ne - nb;
   const int wa = wave & 3;   // position within the group (group A issues K/V)
 
   // K/V DMA sources of group-A wave wa, loads i = 0, 1: unit u = wa·64 + lane
@@ -1296,6 +1487,7 @@ void fa_fwd_kernel_pp(const KParams p) {
       reinterpret_cast<u32x4*>(smem + kPpVBase)[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
   }
+  const int nb = ti.nb, ne = ti.ne, cnt = ne - nb;
 
   const uint32_t ksh = (uint32_t)nb * kBN * (uint32_t)p.k_rs * 2u;
   const uint32_t vsh = (uint32_t)nb * kBN * (uint32_t)p.v_rs * 2u;
@@ -1525,6 +1717,19 @@ static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int 
   if (best < 1) best = 1;
   if (best > nb) best = nb;
   return best;
+}
+
+// Live-range narrowing (narrow_to_live): on for split launches and for the
+// compiled kernel, whose prologue wait covers the probe; off for unsplit
+// launches of the assembly loops, which wait for nothing before their loop, so
+// the probe's memory round trip would be exposed on every workgroup (dense
+// masks: +2 % on cfg2/cfg3). MI355_FA_LIVE=0 turns it off, =1 on everywhere.
+static int live_mode() {
+  static const int f = [] {
+    const char* e = getenv("MI355_FA_LIVE");
+    return (e && (e[0] == '0' || e[0] == '1')) ? e[0] - '0' : 2;
+  }();
+  return f;
 }
 
 // MI355_FA_FUSE=0 keeps the combine launch for every split plan (A/B runs)
@@ -1787,7 +1992,10 @@ static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t 
 }
 
 template <int D, bool BF16>
-static hipError_t launch(const KParams& kp, const CParams& cp, const Plan& pl, hipStream_t st) {
+static hipError_t launch(const KParams& kp_in, const CParams& cp, const Plan& pl, hipStream_t st) {
+  KParams kp = kp_in;
+  const int lm = live_mode();
+  kp.live = pl.num_n >= 4 && (lm == 1 || (lm == 2 && (pl.splits > 1 || !runs_asm_loop<D, BF16>(kp, pl))));
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
   // the fused tail is in the compiled kernel only (the assembly loops keep no
   // registers for it): their split launches keep the combine launch
