@@ -273,6 +273,9 @@ __device__ __forceinline__ float psum8(typename Elt<BF16>::v8 v, float acc) {
 // result is the same softmax: O and l are always scaled by the same factor.
 constexpr float kRescaleSlack = 5.5451774f;   // 8·ln 2
 
+// readfirstlane of a value the caller knows to be uniform
+__device__ __forceinline__ int uni(int x) { return (int)__builtin_amdgcn_readfirstlane((uint32_t)x); }
+
 struct TileIdx {
   int b, h, hk, split, m0, nb, ne;
 };
@@ -282,8 +285,8 @@ struct TileIdx {
 // and the waves of different heads read the same mask rows at the same time.
 // tile_index gives the group's first head; place_wave moves one wave to its
 // head h + w % pack and row slot w / pack.
-template <int BM>
-__device__ __forceinline__ TileIdx tile_index(const KParams& p) {
+template <int BM, class PT>
+__device__ __forceinline__ TileIdx tile_index(PT& p) {
   TileIdx ti;
   int t = xcd_remap(blockIdx.x, p.total);
   const int ng = p.h / p.pack;   // head groups per batch
@@ -329,9 +332,10 @@ __device__ __forceinline__ void place_wave(TileIdx& ti, const KParams& p, int wa
 //    cost is one OR over the workgroup. Otherwise the workgroup reads its rows'
 //    mask from both ends, a window of U whole tiles per end and step (J
 //    16-byte loads per thread and end per round, enough rounds to cover one
-//    tile), ORs the per-tile verdicts over the workgroup and stops on each side
-//    at the first tile with a visible entry: a sliding-window or causal mask
-//    reads its dead edges once. Returns whether the range moved.
+//    tile; once one end is found both windows serve the other), ORs the
+//    per-tile verdicts over the workgroup and stops on each side at the first
+//    tile with a visible entry: a sliding-window or causal mask reads its dead
+//    edges once. Returns whether the range moved.
 // Only entries that are exactly -inf count as blocked; columns >= Sk and rows
 // >= Sq are ignored. A chunk read partly past the end of the buffer reads 0
 // there, i.e. visible: that can only widen the range. Masks whose rows are not
@@ -346,7 +350,22 @@ __device__ __forceinline__ void place_wave(TileIdx& ti, const KParams& p, int wa
 // `red` is 4·waves words of LDS that no DMA touches until the final barrier
 // (two sets, used alternately: a set is rewritten two steps after it was read,
 // past the next barrier).
-__device__ __forceinline__ const KParams& kernarg_params(const KParams& pk) {
+// Read that way (through a generic pointer) the fields count as divergent, so
+// every field that forms a buffer descriptor or a branch goes through
+// readfirstlane: a descriptor the compiler thinks divergent becomes a
+// waterfall loop (one round trip per load), and a branch it thinks divergent
+// makes every value defined under it divergent too.
+typedef const KParams CKParams;
+// A buffer descriptor whose words are uniform but were computed from values
+// the compiler thinks divergent
+__device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo),
+                   __builtin_amdgcn_readfirstlane(bytes));
+}
+__device__ __forceinline__ CKParams& kernarg_params(const KParams& pk) {
 #if defined(__HIP_DEVICE_COMPILE__)
   const KParams* kq = (const KParams*)__builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(kq));
@@ -359,8 +378,10 @@ __device__ __forceinline__ const KParams& kernarg_params(const KParams& pk) {
 // whether the 8 entries of a chunk starting at column c0 hold a visible one
 template <bool BF16>
 __device__ __forceinline__ bool live8(u32x4 v, int c0, int sk) {
-  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u;
+  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u, kNeg2 = kNeg * 0x10001u;
   const int nv = sk - c0;
+  if (nv >= 8)   // a whole chunk: dead iff every word holds two -inf
+    return !(v[0] == kNeg2 && v[1] == kNeg2 && v[2] == kNeg2 && v[3] == kNeg2);
   bool any = false;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -397,14 +418,19 @@ __device__ __forceinline__ void wg_or2(uint32_t& a, uint32_t& b, uint32_t* red, 
   b = __builtin_amdgcn_readfirstlane(rb);
 }
 
+// The mask buffer of batch b
+__device__ __forceinline__ rsrc_t mask_rsrc(CKParams& p, int b) {
+  return make_rsrc_uniform(p.mask + (int64_t)b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+}
+
 struct LiveProbe { u32x4 l, r; };
 
 template <int NT>
 __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams& pk) {
-  const KParams& p = kernarg_params(pk);
+  CKParams& p = kernarg_params(pk);
   LiveProbe pr{};
-  if (!p.live) return pr;
-  const rsrc_t rm = make_rsrc(p.mask + (int64_t)ti.b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+  if (!uni(p.live)) return pr;
+  const rsrc_t rm = mask_rsrc(p, ti.b);
   const int tid = threadIdx.x;
   const uint32_t rowoff = (uint32_t)(ti.m0 + (tid >> 3)) * (uint32_t)p.m_rs + (uint32_t)(tid & 7) * 8u;
   pr.l = bload16(rm, rowoff * 2u);
@@ -412,15 +438,15 @@ __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams
   return pr;
 }
 
-template <bool BF16, int NT, int BMAX, int J>
+template <bool BF16, int NT, int BMAX, int J, bool REUSE>
 __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, int rows, const LiveProbe& pr,
                                                uint32_t* red) {
-  const KParams& p = kernarg_params(pk);
-  if (!p.live) return false;
-  const int nr = min(rows, p.sq - ti.m0);
+  CKParams& p = kernarg_params(pk);
+  if (!uni(p.live)) return false;
+  const int nr = uni(min(rows, p.sq - ti.m0));
   if (nr <= 0) return false;
   const int tid = threadIdx.x;
-  const int nn = p.num_n;
+  const int nn = uni(p.num_n);
   // the probe's verdict: tile 0 / tile nn - 1 live in the chunks it read
   uint32_t lb = (tid < nr * 8 && live8<BF16>(pr.l, (tid & 7) * 8, p.sk)) ? 1u : 0u;
   uint32_t rb = (tid < nr * 8 && live8<BF16>(pr.r, (nn - 1) * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
@@ -434,42 +460,63 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   const int cpt = nr * 8;                  // 16-byte chunks per tile of these rows
   int U = (kRounds * J * NT) / cpt;        // tiles per window: 1 .. 32
   U = U > 32 ? 32 : U;
-  const rsrc_t rm = make_rsrc(p.mask + (int64_t)ti.b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
+  const rsrc_t rm = mask_rsrc(p, ti.b);
   int L = 0, R = nn - 1;
   for (int step = 0; lo < 0 || hi < 0; ++step) {
     if (L > R) break;                      // every tile scanned and dead
-    const int ul = lo < 0 ? min(U, R - L + 1) : 0;
-    const int ur = hi < 0 ? min(U, R - L + 1) : 0;
-    uint32_t lbits = 0u, rbits = 0u;
+    // Two windows of U tile slots. While both ends are open, slots A read
+    // tiles L, L+1, .. and slots B tiles R, R-1, ..; once one end is found,
+    // both windows serve the other end (2U tiles per step).
+    const int rem_t = R - L + 1;
+    const bool both = !REUSE || (lo < 0 && hi < 0), left = lo < 0;
+    // REUSE off (the assembly loops, whose prologue has no SGPRs to spare):
+    // window A serves the left end while it is open, B the right end
+    const int ua = (REUSE || lo < 0) ? min(U, rem_t) : 0;
+    const int ub = both ? ((REUSE || hi < 0) ? min(U, rem_t) : 0) : min(U, max(rem_t - U, 0));
+    // tile of slot t in window A / B: base + dir·t
+    const int da = (!REUSE || left) ? 1 : -1, a0 = (!REUSE || left) ? L : R;
+    const int db = (both || !left) ? -1 : 1, b0 = both ? R : (left ? L + U : R - U);
+    uint32_t abits = 0u, bbits = 0u;
 #pragma unroll
     for (int rd = 0; rd < kRounds; ++rd) {
-      // branch-free: a chunk outside the window loads tile L (in range) and
+      // branch-free: a chunk outside its window loads tile L (in range) and
       // is ignored
-      u32x4 vl[J], vr[J];
+      u32x4 va[J], vb[J];
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         const int c = (rd * J + j) * NT + tid, t = c / cpt, rem = c - t * cpt;
         const uint32_t rowoff = (uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u;
-        vl[j] = bload16(rm, (rowoff + (uint32_t)(t < ul ? L + t : L) * kBN) * 2u);
-        vr[j] = bload16(rm, (rowoff + (uint32_t)(t < ur ? R - t : L) * kBN) * 2u);
+        va[j] = bload16(rm, (rowoff + (uint32_t)(t < ua ? a0 + da * t : L) * kBN) * 2u);
+        vb[j] = bload16(rm, (rowoff + (uint32_t)(t < ub ? b0 + db * t : L) * kBN) * 2u);
       }
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         const int c = (rd * J + j) * NT + tid, t = c / cpt, rem = c - t * cpt;
         const int c0 = (rem & 7) * 8;
         const uint32_t bit = 1u << (t & 31);
-        lbits |= (t < ul && live8<BF16>(vl[j], (L + t) * kBN + c0, p.sk)) ? bit : 0u;
-        rbits |= (t < ur && live8<BF16>(vr[j], (R - t) * kBN + c0, p.sk)) ? bit : 0u;
+        abits |= (t < ua && live8<BF16>(va[j], (a0 + da * t) * kBN + c0, p.sk)) ? bit : 0u;
+        bbits |= (t < ub && live8<BF16>(vb[j], (b0 + db * t) * kBN + c0, p.sk)) ? bit : 0u;
       }
     }
-    wg_or2<NT>(lbits, rbits, red, step & 1);
-    if (lo < 0) { if (lbits) lo = L + __builtin_ctz(lbits); else L += ul; }
-    if (hi < 0) { if (rbits) hi = R - __builtin_ctz(rbits); else R -= ur; }
+    wg_or2<NT>(abits, bbits, red, step & 1);
+    if (both) {
+      if (lo < 0) { if (abits) lo = L + __builtin_ctz(abits); else L += ua; }
+      if (hi < 0) { if (bbits) hi = R - __builtin_ctz(bbits); else R -= ub; }
+    } else if (left) {                     // A: tiles L .. L+ua-1, B: L+U .. L+U+ub-1
+      if (abits) lo = L + __builtin_ctz(abits);
+      else if (bbits) lo = L + U + __builtin_ctz(bbits);
+      else L += ua + ub;
+    } else {                               // A: tiles R .. R-ua+1, B: R-U .. R-U-ub+1
+      if (abits) hi = R - __builtin_ctz(abits);
+      else if (bbits) hi = R - U - __builtin_ctz(bbits);
+      else R -= ua + ub;
+    }
   }
   __syncthreads();                         // every wave has read `red` before any DMA lands
   // no visible entry in these rows: an empty range (lo = 0, hi = -1)
   if (lo < 0) { lo = 0; hi = -1; }
-  const int per = (hi - lo + 1 + p.num_splits - 1) / p.num_splits;
+  const int ns = uni(p.num_splits);
+  const int per = (hi - lo + 1 + ns - 1) / ns;
   const int nb = min(lo + ti.split * per, hi + 1);
   ti.nb = nb;
   ti.ne = min(nb + per, hi + 1);
@@ -518,8 +565,8 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // u = q·k + mask/scale.
 // The row block's ticket word (fused split tail): one per (batch, head group,
 // m-block), shared by that block's splits; ti as tile_index returns it.
-template <int BM>
-__device__ __forceinline__ int ticket_of(const KParams& p, const TileIdx& ti) {
+template <int BM, class PT>
+__device__ __forceinline__ int ticket_of(PT& p, const TileIdx& ti) {
   const int ng = p.h / p.pack;
   return (ti.b * ng + ti.h / p.pack) * p.num_m + ti.m0 / (BM / p.pack);
 }
@@ -611,18 +658,10 @@ __device__ __forceinline__ void fused_tail(float* tl, const uint8_t* stg_lo, con
   constexpr int kS = kFuseMaxSplits;
   static_assert(NT == kS * BM, "one thread per (row, split) LSE");
   uint32_t* flag = reinterpret_cast<uint32_t*>(tl + kS * BM);
-  // The kernel's parameters (its only argument, at the start of the kernarg
-  // segment) are read here, not held in SGPRs from the kernel's entry across
-  // the tile loop: the pointer passes through an empty asm statement, so the
-  // loads cannot be hoisted.
-#if defined(__HIP_DEVICE_COMPILE__)
-  const KParams* kq = (const KParams*)__builtin_amdgcn_kernarg_segment_ptr();
-  asm volatile("" : "+s"(kq));
-#else
-  const KParams* kq = reinterpret_cast<const KParams*>(tl);   // host pass only: never runs
-#endif
-  const KParams& p = *kq;
-  if (!p.fuse) return;
+  // The kernel's parameters are read here through kernarg_params, not held in
+  // SGPRs from the kernel's entry across the tile loop.
+  CKParams& p = kernarg_params(*reinterpret_cast<const KParams*>(tl));
+  if (!uni(p.fuse)) return;
   const TileIdx tb = tile_index<BM>(p);
   const int ticket = ticket_of<BM>(p, tb), b = tb.b, h0 = tb.h, m0 = tb.m0, own = tb.split;
   wait_vmcnt<0>();
@@ -644,11 +683,12 @@ __device__ __forceinline__ void fused_tail(float* tl, const uint8_t* stg_lo, con
   // D elements each, 16-byte units XOR-swizzled by row); the other split's
   // comes by sc1 loads. Weights as in the combine kernel.
   constexpr int CH = D / 8, kTPR = CH, kRPP = NT / kTPR, kPer = BM / kRPP;
-  const int S = p.num_splits;
+  const int S = uni(p.num_splits);
   const int tid = threadIdx.x, c8 = tid % kTPR, rp0 = tid / kTPR;
-  const int rows_h = BM / p.pack;
+  const int rows_h = BM / uni(p.pack);
   const int64_t slab = (int64_t)p.b * p.h * p.sq;
-  const rsrc_t rpart = make_rsrc(p.o_part, p.part_bytes), rlse = make_rsrc(p.lse_part, p.lse_bytes);
+  const rsrc_t rpart = make_rsrc_uniform(p.o_part, p.part_bytes);
+  const rsrc_t rlse = make_rsrc_uniform(p.lse_part, p.lse_bytes);
   auto grow = [&](int rr, int& h, int& m) {
     h = h0 + rr / rows_h;
     m = m0 + rr % rows_h;
@@ -1110,7 +1150,7 @@ void fa_fwd_kernel(const KParams p) {
   {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
-    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8>(tn, p, G::kBM / p.pack, lp,
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true>(tn, p, G::kBM / p.pack, lp,
                                                        reinterpret_cast<uint32_t*>(&sK[NST - 1][0]))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
@@ -1249,7 +1289,7 @@ void fa_fwd_kernel_asm(const KParams p) {
     // before the set-up below: its values would be live across the scan, and
     // the registers the scan needs on top of them would spill
     const LiveProbe lp = live_probe<64 * WAVES>(ti, p);
-    narrow_to_live<BF16, 64 * WAVES, 256, 4>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kAsmMBase));
+    narrow_to_live<BF16, 64 * WAVES, 256, 4, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kAsmMBase));
   }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1417,7 +1457,7 @@ void fa_fwd_kernel_pp(const KParams p) {
     // before the set-up below: its values would be live across the scan, and
     // the SGPRs the scan needs on top of them would spill
     const LiveProbe lp = live_probe<512>(ti, p);
-    narrow_to_live<true, 512, 256, 4>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kPpMBase));
+    narrow_to_live<true, 512, 256, 4, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kPpMBase));
   }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -9,8 +9,12 @@ never produced, and by ``tests/test_isa.py``.
   which the kernels use outside the asm).
 * No packed-FP32 arithmetic (``v_pk_{add,mul,fma}_f32``): the build disables
   the feature; this catches a flag that went missing.
-* No register spills and no scratch memory in any kernel (a kernel that fell
+* No VGPR spills and no scratch memory in any kernel (a kernel that fell
   back to scratch ran 16x slower while still passing every numeric test).
+  SGPR spills are allowed only into VGPR lanes (no scratch) and only outside
+  the MFMA work: every v_writelane / v_readlane of a spill VGPR lies before a
+  kernel's first MFMA or after its last (a few scalar moves in the prologue
+  or epilogue, never in the tile loop).
 * Every kernel's register need fits its workgroup size (waves per SIMD).
 """
 from __future__ import annotations
@@ -44,6 +48,34 @@ def kernel_metadata(text: str):
         yield name.group(1), fields
 
 
+def kernel_body(text: str, name: str) -> list:
+    """Instruction lines of one kernel (from its label to its end marker)."""
+    m = re.search(rf"^{re.escape(name)}:[^\n]*\n(.*?)^\.Lfunc_end", text, re.S | re.M)
+    if not m:
+        return []
+    return [ln.split(";", 1)[0].strip() for ln in m.group(1).splitlines()]
+
+
+def sgpr_spills_in_mfma_span(text: str, name: str) -> list:
+    """Spill moves (v_writelane into a spill VGPR, v_readlane out of one)
+    between the kernel's first and last MFMA; empty when there are none."""
+    body = kernel_body(text, name)
+    if not body:
+        return [f"kernel body of {name} not found"]
+    mf = [i for i, c in enumerate(body) if c.startswith("v_mfma")]
+    lanes = {m.group(1) for c in body for m in [re.match(r"v_writelane_b32\s+(v\d+),", c)] if m}
+    if not mf or not lanes:
+        return []
+    lo, hi = mf[0], mf[-1]
+    bad = []
+    for i in range(lo, hi + 1):
+        c = body[i]
+        m = re.match(r"v_writelane_b32\s+(v\d+),", c) or re.match(r"v_readlane_b32\s+s\d+,\s*(v\d+),", c)
+        if m and m.group(1) in lanes:
+            bad.append(c)
+    return bad
+
+
 def violations(text: str) -> list:
     """Human-readable list of every violated property (empty when clean)."""
     out = []
@@ -56,9 +88,12 @@ def violations(text: str) -> list:
     if pk:
         out.append(f"packed FP32 arithmetic: {pk[:5]}")
     for name, f in kernel_metadata(text):
-        if (int(f.get("vgpr_spill_count", 0)) or int(f.get("sgpr_spill_count", 0))
-                or int(f.get("private_segment_fixed_size", 0))):
+        if int(f.get("vgpr_spill_count", 0)) or int(f.get("private_segment_fixed_size", 0)):
             out.append(f"spills or scratch in {name}: {f}")
+        elif int(f.get("sgpr_spill_count", 0)):
+            bad = sgpr_spills_in_mfma_span(text, name)
+            if bad:
+                out.append(f"SGPR spill code inside the MFMA span of {name}: {bad[:3]}")
     if "scratch_" in "\n".join(code_outside_asm(text)):
         out.append("scratch instructions present")
     # Register need must fit the launch bounds: a SIMD holds 512 registers per
