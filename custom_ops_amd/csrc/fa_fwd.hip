@@ -644,6 +644,27 @@ __device__ __forceinline__ void write_rows(const KParams& p, const f32x16 (&oacc
   }
 }
 
+// Row-block ticket word: a 48-bit launch tag above a 16-bit arrival count.
+// A word holding another tag restarts at 1, so workspace memory left by an
+// earlier launch needs no clearing. A graph replays a captured launch with its
+// captured tag, so within one tag the count runs on: launch instance k takes
+// counts (k-1)·S+1 .. k·S (modulo M = S·floor(65535/S), within 16 bits), and
+// the arrival whose count is a multiple of S is the last of its instance.
+// Returns the new word.
+__device__ __forceinline__ unsigned long long ticket_arrive(unsigned long long* w, unsigned long long tag,
+                                                            int S) {
+  const unsigned long long M = (unsigned long long)S * (65535u / (unsigned)S);
+  unsigned long long old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), nw;
+  do {
+    const unsigned long long c = old & 0xffffull;
+    nw = ((old >> 16) == tag && c < M) ? old + 1 : ((tag << 16) | 1ull);
+  } while (!__hip_atomic_compare_exchange_weak(w, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT));
+  return nw;
+}
+// The count that ends the launch instance an arrival with count c belongs to
+__device__ __forceinline__ int ticket_target(int c, int S) { return ((c - 1) / S + 1) * S; }
+
 // Fused split tail, run by every thread of a split workgroup after its rows'
 // partials are stored (sc1). Once all of them have completed, one lane counts
 // the workgroup in on its row block's ticket; the split that completes the
@@ -667,13 +688,9 @@ __device__ __forceinline__ void fused_tail(float* tl, const uint8_t* stg_lo, con
   wait_vmcnt<0>();
   wg_barrier();
   if (threadIdx.x == 0) {
-    unsigned long long* w = p.tickets + ticket;
-    unsigned long long old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), nw;
-    do {
-      nw = ((old >> 16) == p.tag) ? old + 1 : ((p.tag << 16) | 1ull);
-    } while (!__hip_atomic_compare_exchange_weak(w, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT));
-    *flag = ((nw & 0xffffull) == (unsigned long long)p.num_splits) ? 1u : 0u;
+    const int S = p.num_splits;
+    const int c = (int)(ticket_arrive(p.tickets + ticket, p.tag, S) & 0xffffull);
+    *flag = (c == ticket_target(c, S)) ? 1u : 0u;
   }
   wg_barrier();
   if (*flag == 0u) return;

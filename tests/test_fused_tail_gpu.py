@@ -1,10 +1,11 @@
 """The fused split tail (two-split launches of the compiled kernel: the last
 split of each row block combines it, no combine launch) against the same
 launches with the combine kernel (MI355_FA_FUSE=0), bit for bit, and against
-the fp32 torch restatement of the reference op. Each setting runs in a fresh
-process (the switch is read once per process). Every case is called three
-times on one workspace, so ticket words left by earlier launches are
-exercised; the outputs of the three calls must agree bit for bit.
+the fp32 torch restatement of the reference op; launches of 3 and 7 splits
+(combine launch either way) ride along. Each setting runs in a fresh process
+(the switch is read once per process). Every case is called three times on
+one workspace, so ticket words left by earlier launches are exercised; the
+outputs of the three calls must agree bit for bit.
 """
 import os
 import subprocess
@@ -41,14 +42,15 @@ CODE = textwrap.dedent("""
         m = m.masked_fill((j < i) | (torch.rand(b, 1, sq, sk, generator=g) < 0.1), float("-inf"))
         m[:, :, 5, :] = float("-inf")
         m = m.to(dt).cuda()
-        outs = [mha_fwd_with_mask(q, k, v, m, num_splits=2) for _ in range(3)]
-        torch.cuda.synchronize()
         ref = ref_attn_torch(q, k, v, m)
-        for o in outs:
-            assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16)), "repeat calls differ"
-        assert_close(outs[0], ref, f"fused-tail case {(b, hq, hk, sq, sk, d, dt, waves)}")
-        assert bool((outs[0][:, :, 5] == 0).all())
-        h.update(outs[0].view(torch.int16).cpu().numpy().tobytes())
+        for splits in (2, 3, 7):
+            outs = [mha_fwd_with_mask(q, k, v, m, num_splits=splits) for _ in range(3)]
+            torch.cuda.synchronize()
+            for o in outs:
+                assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16)), "repeat calls differ"
+            assert_close(outs[0], ref, f"fused-tail case {(b, hq, hk, sq, sk, d, dt, waves, splits)}")
+            assert bool((outs[0][:, :, 5] == 0).all())
+            h.update(outs[0].view(torch.int16).cpu().numpy().tobytes())
     print("HASH", h.hexdigest())
 """)
 
