@@ -94,11 +94,40 @@ def build_probe(verbose: bool = False) -> str:
     return PROBE_PATH
 
 
+TORCH_BINDING_SRC = os.path.join(PKG_DIR, "csrc", "torch_binding.cpp")
+TORCH_BINDING_PATH = os.path.join(PKG_DIR, "libmi355_fa_torch.so")
+
+
+def build_torch_binding(verbose: bool = False) -> str:
+    """Compile the C++ torch extension over the C ABI (csrc/torch_binding.cpp:
+    the reference-style TORCH_LIBRARY binding) against this PyTorch-ROCm, linked
+    to libmi355_fa.so next to it. Host code only, so the host compiler builds it."""
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    abi = int(torch.compiled_with_cxx11_abi())
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-DUSE_ROCM", "-D__HIP_PLATFORM_AMD__",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-I{tdir}/include",
+           f"-I{tdir}/include/torch/csrc/api/include", "-I/opt/rocm/include", f"-I{INCLUDE}",
+           TORCH_BINDING_SRC, "-o", TORCH_BINDING_PATH + ".tmp",
+           f"-L{tdir}/lib", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+           "-L/opt/rocm/lib", "-lamdhip64", f"-L{PKG_DIR}", "-lmi355_fa", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch binding build failed ({res.returncode}):\n{res.stderr[-4000:]}")
+    os.replace(TORCH_BINDING_PATH + ".tmp", TORCH_BINDING_PATH)
+    return TORCH_BINDING_PATH
+
+
 def build(verbose: bool = False) -> str:
-    """Compile the library (always recompiles) and the measurement probe;
-    return the library's path."""
+    """Compile the library (always recompiles), the C++ torch binding over it
+    and the measurement probe; return the library's path."""
     build_probe(verbose=verbose)
-    return compile_checked(LIB_PATH, verbose=verbose)
+    out = compile_checked(LIB_PATH, verbose=verbose)
+    build_torch_binding(verbose=verbose)
+    return out
 
 
 if __name__ == "__main__":
