@@ -378,15 +378,15 @@ __device__ __forceinline__ CKParams& kernarg_params(const KParams& pk) {
 // whether the 8 entries of a chunk starting at column c0 hold a visible one
 template <bool BF16>
 __device__ __forceinline__ bool live8(u32x4 v, int c0, int sk) {
-  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u, kNeg2 = kNeg * 0x10001u;
+  // branch-free (a branch here lets the compiler sink a window load into it,
+  // behind the step's wait: a second round trip per step)
+  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u;
   const int nv = sk - c0;
-  if (nv >= 8)   // a whole chunk: dead iff every word holds two -inf
-    return !(v[0] == kNeg2 && v[1] == kNeg2 && v[2] == kNeg2 && v[3] == kNeg2);
   bool any = false;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t x = (v[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-    any |= (e < nv) && (x != kNeg);
+  for (int i = 0; i < 4; ++i) {
+    any |= (2 * i < nv) & ((v[i] & 0xffffu) != kNeg);
+    any |= (2 * i + 1 < nv) & ((v[i] >> 16) != kNeg);
   }
   return any;
 }
@@ -446,10 +446,10 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   const int nr = uni(min(rows, p.sq - ti.m0));
   if (nr <= 0) return false;
   const int tid = threadIdx.x;
-  const int nn = uni(p.num_n);
+  const int nn = p.num_n;   // the scan's control stays in VGPRs: no SGPRs to spare here
   // the probe's verdict: tile 0 / tile nn - 1 live in the chunks it read
-  uint32_t lb = (tid < nr * 8 && live8<BF16>(pr.l, (tid & 7) * 8, p.sk)) ? 1u : 0u;
-  uint32_t rb = (tid < nr * 8 && live8<BF16>(pr.r, (nn - 1) * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
+  uint32_t lb = ((tid < nr * 8) & live8<BF16>(pr.l, (tid & 7) * 8, p.sk)) ? 1u : 0u;
+  uint32_t rb = ((tid < nr * 8) & live8<BF16>(pr.r, (nn - 1) * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
   wg_or2<NT>(lb, rb, red, 1);
   if (lb && rb) {                          // whole axis live: the nominal ranges stand
     __syncthreads();                       // every wave has read `red` before any DMA lands
@@ -461,6 +461,19 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   int U = (kRounds * J * NT) / cpt;        // tiles per window: 1 .. 32
   U = U > 32 ? 32 : U;
   const rsrc_t rm = mask_rsrc(p, ti.b);
+  // Each thread's chunks, the same in every step: window slot t, row offset
+  // and column within the tile (one division each, here, not per step)
+  constexpr int NL = kRounds * J;
+  int tj[NL];
+  uint32_t roff[NL];
+#pragma unroll
+  for (int n = 0; n < NL; ++n) {
+    const int c = n * NT + tid, t = c / cpt, rem = c - t * cpt;
+    tj[n] = t;
+    roff[n] = (uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u;
+  }
+  const int c0 = (tid & 7) * 8;   // NT and cpt are multiples of 8: rem & 7 == tid & 7
+  const int sk = p.sk;
   int L = 0, R = nn - 1;
   for (int step = 0; lo < 0 || hi < 0; ++step) {
     if (L > R) break;                      // every tile scanned and dead
@@ -477,26 +490,21 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
     const int da = (!REUSE || left) ? 1 : -1, a0 = (!REUSE || left) ? L : R;
     const int db = (both || !left) ? -1 : 1, b0 = both ? R : (left ? L + U : R - U);
     uint32_t abits = 0u, bbits = 0u;
+    // branch-free: a chunk outside its window loads tile L (in range) and is
+    // ignored
+    u32x4 va[NL], vb[NL];
 #pragma unroll
-    for (int rd = 0; rd < kRounds; ++rd) {
-      // branch-free: a chunk outside its window loads tile L (in range) and
-      // is ignored
-      u32x4 va[J], vb[J];
+    for (int n = 0; n < NL; ++n) {
+      const int t = tj[n];
+      va[n] = bload16(rm, (roff[n] + (uint32_t)(t < ua ? a0 + da * t : L) * kBN) * 2u);
+      vb[n] = bload16(rm, (roff[n] + (uint32_t)(t < ub ? b0 + db * t : L) * kBN) * 2u);
+    }
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int c = (rd * J + j) * NT + tid, t = c / cpt, rem = c - t * cpt;
-        const uint32_t rowoff = (uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u;
-        va[j] = bload16(rm, (rowoff + (uint32_t)(t < ua ? a0 + da * t : L) * kBN) * 2u);
-        vb[j] = bload16(rm, (rowoff + (uint32_t)(t < ub ? b0 + db * t : L) * kBN) * 2u);
-      }
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int c = (rd * J + j) * NT + tid, t = c / cpt, rem = c - t * cpt;
-        const int c0 = (rem & 7) * 8;
-        const uint32_t bit = 1u << (t & 31);
-        abits |= (t < ua && live8<BF16>(va[j], (a0 + da * t) * kBN + c0, p.sk)) ? bit : 0u;
-        bbits |= (t < ub && live8<BF16>(vb[j], (b0 + db * t) * kBN + c0, p.sk)) ? bit : 0u;
-      }
+    for (int n = 0; n < NL; ++n) {
+      const int t = tj[n];
+      const uint32_t bit = 1u << (t & 31);
+      abits |= ((t < ua) & live8<BF16>(va[n], (a0 + da * t) * kBN + c0, sk)) ? bit : 0u;
+      bbits |= ((t < ub) & live8<BF16>(vb[n], (b0 + db * t) * kBN + c0, sk)) ? bit : 0u;
     }
     wg_or2<NT>(abits, bbits, red, step & 1);
     if (both) {
