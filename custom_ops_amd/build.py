@@ -60,6 +60,12 @@ def compile_checked(out_path: str, flags=None, verbose: bool = False) -> str:
         res = subprocess.run(cmd, capture_output=True, text=True, cwd=tmp)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+        # A kernel that misses its amdgpu_waves_per_eu target has lost the
+        # occupancy its tiling was designed for (registers past the budget,
+        # or LDS that no longer lets two workgroups share a CU).
+        missed = [l for l in res.stderr.splitlines() if "failed to meet occupancy target" in l]
+        if missed:
+            raise RuntimeError("occupancy target missed; library not installed:\n" + "\n".join(missed[:8]))
         asm = sorted(glob.glob(os.path.join(tmp, "*amdgcn-amd-amdhsa*.s")))
         if not asm:
             raise RuntimeError("hipcc left no device assembly to check")

@@ -1135,8 +1135,15 @@ void fa_fwd_kernel(const KParams p) {
   __shared__ __align__(16) uint16_t sK[NST][G::kKElems];
   __shared__ __align__(16) uint16_t sV[NST][G::kVElems];
   __shared__ __align__(16) uint16_t sM[A::MREG ? 8 : G::kMElems];
-  // fused split tail: per (split, row) LSEs then weights, and the ticket flag
-  __shared__ __align__(16) float sTail[SPLIT ? kFuseMaxSplits * G::kBM + 4 : 4];
+  // fused split tail: per (split, row) LSEs then weights, and the ticket flag.
+  // 4 waves: in the V stages, which the output staging leaves free. An array
+  // of its own would take the workgroup past 80 KiB of LDS, so two could no
+  // longer share a CU and the compiler, no longer held to two waves per SIMD,
+  // would spend registers past 256 (and AGPR copies in the tile loop).
+  constexpr bool kTailOwn = SPLIT && WAVES == 8;
+  constexpr int kTailFloats = kFuseMaxSplits * G::kBM + 4;
+  static_assert(kTailOwn || !SPLIT || kTailFloats * 4 <= NST * G::kVElems * 2, "tail fits in the V stages");
+  __shared__ __align__(16) float sTail[kTailOwn ? kTailFloats : 1];
 
   TileIdx ti = tile_index<G::kBM>(p);
   const TileIdx tg = ti;   // the workgroup's first head and row
@@ -1264,7 +1271,8 @@ void fa_fwd_kernel(const KParams p) {
                  + (a.wave & 3) * 32 * D * 2;
   a.epilogue(ti.b, ti.h, ti.split, qrow, stg);
   if constexpr (SPLIT)
-    fused_tail<D, BF16, G::kBM, G::kThreads>(sTail, reinterpret_cast<const uint8_t*>(&sK[0][0]),
+    fused_tail<D, BF16, G::kBM, G::kThreads>(kTailOwn ? sTail : reinterpret_cast<float*>(&sV[0][0]),
+                                             reinterpret_cast<const uint8_t*>(&sK[0][0]),
                                              reinterpret_cast<const uint8_t*>(&sV[0][0]));
 }
 
