@@ -50,7 +50,7 @@ def hipcc() -> str:
 def compile_checked(out_path: str, flags=None, verbose: bool = False) -> str:
     """Compile SRC into ``out_path`` (atomically) after checking the device
     assembly of that same compilation; raise RuntimeError on either failure."""
-    from .isa_check import violations
+    from .isa_check import missed_occupancy, violations
     flags = list(HIPCC_FLAGS if flags is None else flags)
     with tempfile.TemporaryDirectory(prefix="mi355fa-build-") as tmp:
         product = os.path.join(tmp, os.path.basename(out_path))
@@ -63,7 +63,7 @@ def compile_checked(out_path: str, flags=None, verbose: bool = False) -> str:
         # A kernel that misses its amdgpu_waves_per_eu target has lost the
         # occupancy its tiling was designed for (registers past the budget,
         # or LDS that no longer lets two workgroups share a CU).
-        missed = [l for l in res.stderr.splitlines() if "failed to meet occupancy target" in l]
+        missed = missed_occupancy(res.stderr)
         if missed:
             raise RuntimeError("occupancy target missed; library not installed:\n" + "\n".join(missed[:8]))
         asm = sorted(glob.glob(os.path.join(tmp, "*amdgcn-amd-amdhsa*.s")))

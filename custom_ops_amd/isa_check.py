@@ -16,6 +16,11 @@ never produced, and by ``tests/test_isa.py``.
   kernel's first MFMA or after its last (a few scalar moves in the prologue
   or epilogue, never in the tile loop).
 * Every kernel's register need fits its workgroup size (waves per SIMD).
+* The compiled kernel (``fa_fwd_kernel``) moves nothing through AGPRs: its
+  accumulators live in VGPRs, and ``v_accvgpr_read/write`` there means the
+  compiler ran past its register budget and copies scores or O through AGPRs
+  on every tile (VALU issue the HBM-streaming plans cannot hide). The
+  assembly loops keep Q and O in AGPRs by design and are not checked.
 """
 from __future__ import annotations
 
@@ -94,6 +99,10 @@ def violations(text: str) -> list:
             bad = sgpr_spills_in_mfma_span(text, name)
             if bad:
                 out.append(f"SGPR spill code inside the MFMA span of {name}: {bad[:3]}")
+        if "13fa_fwd_kernelI" in name:
+            agpr = [ln for ln in kernel_body(text, name) if ln.startswith("v_accvgpr_")]
+            if agpr:
+                out.append(f"AGPR copies in the compiled kernel {name}: {len(agpr)}, e.g. {agpr[0]}")
     if "scratch_" in "\n".join(code_outside_asm(text)):
         out.append("scratch instructions present")
     # Register need must fit the launch bounds: a SIMD holds 512 registers per
@@ -110,3 +119,10 @@ def violations(text: str) -> list:
                 out.append(f"{m.group(1)} needs {nf.group(1)} registers per wave but its "
                            f"{wg}-thread workgroup puts {per_simd} waves on a SIMD")
     return out
+
+
+def missed_occupancy(stderr: str) -> list:
+    """hipcc's reports of kernels that missed their ``amdgpu_waves_per_eu``
+    target (registers past the budget, or LDS that no longer lets the planned
+    number of workgroups share a CU)."""
+    return [ln.strip() for ln in stderr.splitlines() if "failed to meet occupancy target" in ln]

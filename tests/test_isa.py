@@ -102,6 +102,33 @@ def test_checker_sgpr_spills_only_outside_the_mfma_span(pre, mid, post, ok):
     assert (found == []) == ok, found
 
 
+_AGPR = """\
+	;;#ASMSTART
+	s_mov_b32 m0, s1
+	;;#ASMEND
+{name}:                                      ; @k
+	v_mfma_f32_32x32x16_bf16 v[0:15], v[16:19], v[20:23], v[0:15]
+{body}
+	s_endpgm
+.Lfunc_end0:
+amdhsa.kernels:
+  - .name:           {name}
+    .private_segment_fixed_size: 0
+    .sgpr_spill_count: 0
+    .vgpr_spill_count: 0
+"""
+
+
+@pytest.mark.parametrize("name,body,ok", [
+    ("_ZN7mi355fa13fa_fwd_kernelILi128ELb1ELb1ELb1ELi4EEEvNS_7KParamsE", "\tv_mul_f32 v1, v2, v3", True),
+    ("_ZN7mi355fa13fa_fwd_kernelILi128ELb1ELb1ELb1ELi4EEEvNS_7KParamsE", "\tv_accvgpr_read_b32 v1, a7", False),
+    ("_ZN7mi355fa17fa_fwd_kernel_asmILi1ELb1ELb0EEEvNS_7KParamsE", "\tv_accvgpr_read_b32 v1, a7", True),
+])
+def test_checker_catches_agpr_copies_in_the_compiled_kernel(name, body, ok):
+    found = [v for v in violations(_AGPR.format(name=name, body=body)) if "AGPR copies" in v]
+    assert (found == []) == ok, found
+
+
 _REGFIT = """\
 \t.amdhsa_kernel k
 \t\t.amdhsa_next_free_vgpr {nf}
@@ -195,3 +222,13 @@ def test_register_declaration_check_catches_an_undeclared_write():
            '#define MI355_X_CLOBBERS_BF16 "v6", "s69"\n')
     decl, wrote = _declared_and_written(inc)["X_BF16"]
     assert wrote["v"] - decl["v"] == {7} and wrote["s"] - decl["s"] == {70}
+
+
+def test_missed_occupancy_target_is_reported():
+    from custom_ops_amd.isa_check import missed_occupancy
+    err = ("warning: <unknown>:0:0: failed to meet occupancy target given by 'amdgpu-waves-per-eu' in "
+           "'k': desired occupancy was 2, final occupancy is 1 [-Wpass-failed]\n"
+           "warning: inline asm clobber list contains reserved registers: M0\n")
+    assert len(missed_occupancy(err)) == 1
+    assert missed_occupancy("warning: inline asm clobber list contains reserved registers: M0\n") == []
+
