@@ -185,6 +185,9 @@ struct KParams {
   int fuse;
   uint32_t part_bytes, lse_bytes;   // sizes of o_part and lse_part (fuse: both below 2^31)
   int live;   // narrow each workgroup's key range to its live tiles
+  // bf16, scale < 0.99: the compiled kernel's LDS mask path adds the mask on
+  // the matrix core (bf16(1/scale) > 1.0078 makes -max_bf16 overflow to -inf)
+  int mask_mfma;
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -800,6 +803,17 @@ struct Attn {
   // per-row register loads (32 cache lines per instruction) cost more than
   // the LDS round trip.
   static constexpr bool MREG = MDIRECT && WAVES == 8;
+  // LDS mask path with bf16 data: the mask can be added on the matrix core
+  // (p.mask_mfma): u = A_0·M_0 + A_1·M_1 per 32-key block, where M_c is the
+  // 16-key chunk c of the block (keys 16c + 8g .. +7 of the lane's row, the B
+  // operand as it sits in LDS) and A_c selects each score's key with weight
+  // bf16(1/scale) (A_c[row i][k] = bf16(1/scale) where key π(i) = 16c + k).
+  // -inf is first clamped to -max_bf16 (0 × -inf would be NaN); -max·w
+  // overflows the fp32 sum back to -inf for w > 1.0078. Masks of 0 and -inf
+  // give the same scores as the VALU widening, bit for bit.
+  static constexpr bool MMF = BF16 && !MREG;
+  bool mmfma = false;
+  V8 msel[MMF ? 2 : 1];
   uint32_t m_off[MREG ? 1 : G::kMWaveLoads];
   uint32_t k_rd[KD];
   uint32_t v_rd[DB];
@@ -848,10 +862,24 @@ struct Attn {
         m_off[i] = (uint32_t)((ti.m0 + m) * p.m_rs + (slot ^ mask_swz(m)) * 8) * 2u;
       }
       const int mr = wave * 32 + l32;
+      mmfma = MMF && uni(p.mask_mfma) != 0;
 #pragma unroll
       for (int i = 0; i < 2 * NKB; ++i) {
-        const int u = (i / 2) * 4 + 2 * g + (i % 2);
+        // the lane's own keys 16g + 8(i%2) of block i/2, or (matrix-core add)
+        // chunk i%2 of the block: keys 16(i%2) + 8g
+        const int u = mmfma ? (i / 2) * 4 + 2 * (i % 2) + g : (i / 2) * 4 + 2 * g + (i % 2);
         m_rd[i] = (uint32_t)(mr * kBN + ((u ^ mask_swz(mr)) * 8)) * 2u;
+      }
+      if constexpr (MMF) {
+        const uint32_t sb = (uint32_t)bitcast<uint16_t>((__bf16)(1.f / p.scale));
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int e = key_perm(l32) - 16 * c - 8 * g;
+          u32x4 w;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = (e == 2 * j) ? sb : (e == 2 * j + 1) ? (sb << 16) : 0u;
+          msel[c] = bitcast<V8>(w);
+        }
       }
     }
     {
@@ -967,6 +995,24 @@ struct Attn {
   __device__ __forceinline__ void mask_init(const uint16_t* sM) { mask_init(sM, s); }
   __device__ __forceinline__ void mask_init(const uint16_t* sM, Scores& sc) {
     const uint8_t* mb = reinterpret_cast<const uint8_t*>(sM);
+    if constexpr (MMF) {
+      if (mmfma) {
+        typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+        const us2 lim = {0xff7fu, 0xff7fu};   // -max_bf16: -inf (0xff80) and above clamp to it
+#pragma unroll
+        for (int b = 0; b < NKB; ++b) {
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            u32x4 x = *reinterpret_cast<const u32x4*>(mb + m_rd[2 * b + c]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              x[j] = bitcast<uint32_t>(__builtin_elementwise_min(bitcast<us2>(x[j]), lim));
+            sc[b] = Elt<BF16>::mfma(msel[c], bitcast<V8>(x), c == 0 ? f32x16{} : sc[b]);
+          }
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int b = 0; b < NKB; ++b) {
       u32x4 lo, hi;
@@ -2171,6 +2217,10 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.num_splits = pl.splits; kp.n_per_split = pl.n_per_split;
   kp.total = (int)total;
   kp.scale = p->scale_softmax;
+  {
+    const char* e = getenv("MI355_FA_MASK_MFMA");   // tuning override: 0 widens the mask on the VALU
+    kp.mask_mfma = (p->dtype == MI355_FA_BF16 && p->scale_softmax < 0.99f && !(e && e[0] == '0')) ? 1 : 0;
+  }
   {
     const float c2 = p->scale_softmax * kLog2e, slack = kRescaleSlack / p->scale_softmax;
     memcpy(&kp.c2_bits, &c2, 4);
