@@ -1170,16 +1170,29 @@ struct Attn {
 #define MI355_FA_STAGES4 2
 #endif
 // Two waves per SIMD: the 8-wave workgroup alone, or two 4-wave workgroups
-// (80 KiB of LDS each at two stages) sharing a CU.
-template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES>
+// (80 KiB of LDS each at two stages) sharing a CU. DEEP (4 waves, grids of at
+// most one workgroup per CU): a third K/V stage, in dynamic LDS, so the
+// compiler still budgets registers for two waves per SIMD (static LDS past
+// 80 KiB would lift that target and cost AGPR copies in the tile loop).
+template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES, bool DEEP>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
   typedef Attn<D, BF16, SPLIT, MDIRECT, WAVES> A;
-  constexpr int NST = WAVES == 8 ? MI355_FA_STAGES8 : MI355_FA_STAGES4;
+  constexpr int NST = WAVES == 8 ? MI355_FA_STAGES8
+                                 : (DEEP && MI355_FA_STAGES4 < 3 ? 3 : MI355_FA_STAGES4);
   static_assert(NST >= 2 && NST <= 4, "two to four stages");
-  __shared__ __align__(16) uint16_t sK[NST][G::kKElems];
-  __shared__ __align__(16) uint16_t sV[NST][G::kVElems];
+  static_assert(!DEEP || WAVES == 4, "the deep pipeline is a 4-wave variant");
+  constexpr int NSS = DEEP ? 2 : NST;   // stages in static LDS; the rest follow in dynamic LDS
+  __shared__ __align__(16) uint16_t sKs[NSS][G::kKElems];
+  __shared__ __align__(16) uint16_t sVs[NSS][G::kVElems];
+  extern __shared__ __align__(16) uint16_t fa_dyn_lds[];   // DEEP: [K stage | V stage] per extra stage
+  auto KS = [&](int i) -> uint16_t* {
+    return i < NSS ? sKs[i] : fa_dyn_lds + (i - NSS) * (G::kKElems + G::kVElems);
+  };
+  auto VS = [&](int i) -> uint16_t* {
+    return i < NSS ? sVs[i] : fa_dyn_lds + (i - NSS) * (G::kKElems + G::kVElems) + G::kKElems;
+  };
   __shared__ __align__(16) uint16_t sM[A::MREG ? 8 : G::kMElems];
   // fused split tail: per (split, row) LSEs then weights, and the ticket flag.
   // 4 waves: in the V stages, which the output staging leaves free. An array
@@ -1188,7 +1201,7 @@ void fa_fwd_kernel(const KParams p) {
   // would spend registers past 256 (and AGPR copies in the tile loop).
   constexpr bool kTailOwn = SPLIT && WAVES == 8;
   constexpr int kTailFloats = kFuseMaxSplits * G::kBM + 4;
-  static_assert(kTailOwn || !SPLIT || kTailFloats * 4 <= NST * G::kVElems * 2, "tail fits in the V stages");
+  static_assert(kTailOwn || !SPLIT || kTailFloats * 4 <= NSS * G::kVElems * 2, "tail fits in the V stages");
   __shared__ __align__(16) float sTail[kTailOwn ? kTailFloats : 1];
 
   TileIdx ti = tile_index<G::kBM>(p);
@@ -1208,7 +1221,7 @@ void fa_fwd_kernel(const KParams p) {
   if (p.sk % kBN != 0) {
     for (int i = threadIdx.x; i < G::kVElems / 8; i += G::kThreads)
 #pragma unroll
-      for (int st = 0; st < NST; ++st) reinterpret_cast<u32x4*>(sV[st])[i] = u32x4{0u, 0u, 0u, 0u};
+      for (int st = 0; st < NST; ++st) reinterpret_cast<u32x4*>(VS(st))[i] = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
   }
   int cnt = ne - nb;
@@ -1217,8 +1230,8 @@ void fa_fwd_kernel(const KParams p) {
 #pragma unroll
     for (int j = 0; j < NST - 1; ++j) {
       if (j < cnt) {
-        a.issue_k(nb + j, sK[j]);
-        a.issue_v(nb + j, sV[j]);
+        a.issue_k(nb + j, KS(j));
+        a.issue_v(nb + j, VS(j));
       }
     }
   };
@@ -1229,7 +1242,7 @@ void fa_fwd_kernel(const KParams p) {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
     if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true>(tn, p, G::kBM / p.pack, lp,
-                                                       reinterpret_cast<uint32_t*>(&sK[NST - 1][0]))) {
+                                                       reinterpret_cast<uint32_t*>(KS(NST - 1)))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
       ne = tn.ne;
@@ -1263,15 +1276,15 @@ void fa_fwd_kernel(const KParams p) {
     // reads do not share the LDS with the incoming K tile (cfg2 -1.4 %,
     // cfg5 -3.5 %; measured +3 % on cfg4 in the 4-wave kernel).
     if constexpr (WAVES == 4) {
-      if (far) a.issue_k(n + NST - 1, sK[SF]);
+      if (far) a.issue_k(n + NST - 1, KS(SF));
     }
-    a.qk(sK[ST]);
+    a.qk(KS(ST));
     if constexpr (WAVES == 8) {
-      if (far) a.issue_k(n + NST - 1, sK[SF]);
+      if (far) a.issue_k(n + NST - 1, KS(SF));
     }
-    if (far) a.issue_v(n + NST - 1, sV[SF]);
+    if (far) a.issue_v(n + NST - 1, VS(SF));
     a.apply_tail(n);
-    a.softmax_pv(sV[ST]);
+    a.softmax_pv(VS(ST));
     if constexpr (A::MREG) {
       // widen mask(n + 1) into the accumulators (the compiler waits for its
       // loads, and with them for the K/V DMAs issued later). Kept inside this
@@ -1309,17 +1322,17 @@ void fa_fwd_kernel(const KParams p) {
 
   // The K/V stages are free once every wave is past its last tile (and no
   // DMA is in flight): each wave stages its output rows in a private slice.
-  static_assert(4 * 32 * D * 2 <= NST * G::kKElems * 2 && 4 * 32 * D * 2 <= NST * G::kVElems * 2,
+  static_assert(4 * 32 * D * 2 <= NSS * G::kKElems * 2 && 4 * 32 * D * 2 <= NSS * G::kVElems * 2,
                 "output staging fits in the K and V stages");
   wait_vmcnt<0>();
   wg_barrier();
-  uint8_t* stg = (a.wave < 4 ? reinterpret_cast<uint8_t*>(&sK[0][0]) : reinterpret_cast<uint8_t*>(&sV[0][0]))
+  uint8_t* stg = (a.wave < 4 ? reinterpret_cast<uint8_t*>(KS(0)) : reinterpret_cast<uint8_t*>(VS(0)))
                  + (a.wave & 3) * 32 * D * 2;
   a.epilogue(ti.b, ti.h, ti.split, qrow, stg);
   if constexpr (SPLIT)
-    fused_tail<D, BF16, G::kBM, G::kThreads>(kTailOwn ? sTail : reinterpret_cast<float*>(&sV[0][0]),
-                                             reinterpret_cast<const uint8_t*>(&sK[0][0]),
-                                             reinterpret_cast<const uint8_t*>(&sV[0][0]));
+    fused_tail<D, BF16, G::kBM, G::kThreads>(kTailOwn ? sTail : reinterpret_cast<float*>(VS(0)),
+                                             reinterpret_cast<const uint8_t*>(KS(0)),
+                                             reinterpret_cast<const uint8_t*>(VS(0)));
 }
 
 // ── software-pipelined tile loop in generated assembly (d = 128) ─────────────
@@ -1866,6 +1879,7 @@ struct Plan {
   int head_major;
   size_t o_part_bytes, lse_bytes, ticket_bytes, ws_bytes;
   int fuse;   // split tail fused into the main kernel (no combine launch)
+  int deep;   // 4 waves, at most one workgroup per CU: three K/V stages
 };
 
 // Tile plan: the workgroup size (4 or 8 waves) and split count with the
@@ -1989,6 +2003,16 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
               fuse_enabled();
   }
   pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
+  // A 4-wave grid that puts at most one workgroup on each CU takes a third K/V
+  // stage (112 KiB of LDS at d = 128: one workgroup per CU; cfg4 cold -7 %).
+  {
+    static const bool deep_on = [] {
+      const char* e = getenv("MI355_FA_DEEP");   // tuning override: 0 keeps two stages
+      return !(e && e[0] == '0');
+    }();
+    const int64_t wgs = (int64_t)p->b * (p->h / pl.pack) * pl.num_m * s;
+    pl.deep = (pl.waves == 4 && wgs <= cus && deep_on) ? 1 : 0;
+  }
   return pl;
 }
 
@@ -2041,14 +2065,16 @@ static int validate(const mi355_fa_params* p, char* err, size_t errlen) {
   return MI355_FA_OK;
 }
 
-template <int D, bool BF16, bool SPLIT, int WAVES>
+template <int D, bool BF16, bool SPLIT, int WAVES, bool DEEP>
 static hipError_t launch_main(const KParams& kp, hipStream_t st) {
+  constexpr int NST = WAVES == 8 ? MI355_FA_STAGES8 : (DEEP && MI355_FA_STAGES4 < 3 ? 3 : MI355_FA_STAGES4);
+  const size_t dyn = DEEP ? (size_t)(NST - 2) * (Geo<D, WAVES>::kKElems + Geo<D, WAVES>::kVElems) * 2 : 0;
   if (kp.mask_direct)
-    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, true, WAVES>), dim3(kp.total),
-                       dim3(64 * WAVES), 0, st, kp);
+    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, true, WAVES, DEEP>), dim3(kp.total),
+                       dim3(64 * WAVES), dyn, st, kp);
   else
-    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, false, WAVES>), dim3(kp.total),
-                       dim3(64 * WAVES), 0, st, kp);
+    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, false, WAVES, DEEP>), dim3(kp.total),
+                       dim3(64 * WAVES), dyn, st, kp);
   return hipGetLastError();
 }
 
@@ -2106,8 +2132,8 @@ static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t 
       return hipGetLastError();
     }
   }
-  return pl.waves == 8 ? launch_main<D, BF16, SPLIT, 8>(kp, st)
-                       : launch_main<D, BF16, SPLIT, 4>(kp, st);
+  if (pl.waves == 8) return launch_main<D, BF16, SPLIT, 8, false>(kp, st);
+  return pl.deep ? launch_main<D, BF16, SPLIT, 4, true>(kp, st) : launch_main<D, BF16, SPLIT, 4, false>(kp, st);
 }
 
 template <int D, bool BF16>
