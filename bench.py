@@ -22,9 +22,11 @@ events on the op's stream. Prints ONE JSON line:
                  reference's way (a 256 MB buffer zeroed before each iteration,
                  median, benchmark/benchmark_fa.py:115-132), "us_hot"
   cpu_baseline = PyTorch fp32 math attention on this host's cores over a
-                 bounded sample of whole (b, h) heads of every config; each
-                 config timed 3 times in the same order and thread count, the
-                 median reported with its spread; value = the cfg2 row.
+                 bounded sample of whole (b, h) heads of every config; the
+                 threads pinned to a fixed set of cores; per config one
+                 untimed repetition, then 5 timed ones in the same order and
+                 thread count, the median reported with its spread; value =
+                 the cfg2 row.
 """
 import argparse
 import json
@@ -49,8 +51,8 @@ def parse():
     ap.add_argument("--settle-s", type=float, default=0.5,
                     help="untimed back-to-back steps before warmup, in seconds (clock ramp)")
     ap.add_argument("--ref-iters", type=int, default=50)
-    ap.add_argument("--cpu-seconds", type=float, default=3.0,
-                    help="CPU work per config per repetition (3 repetitions)")
+    ap.add_argument("--cpu-seconds", type=float, default=2.0,
+                    help="CPU work per config per repetition (1 untimed + 5 timed repetitions)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
     return ap.parse_args()
@@ -107,22 +109,30 @@ def _cpu_name() -> str:
     return platform.processor() or ""
 
 
-def cpu_baseline(seconds: float, reps: int = 3):
+def cpu_baseline(seconds: float, reps: int = 5):
     """PyTorch fp32 math attention (the reference's CPU path) on host cores.
 
-    For every config, in a fixed order: whole (b, h) heads are timed ``reps``
-    times; the head count per repetition is fixed by a probe so that one
-    repetition takes about ``seconds`` (all heads if they fit). Each
+    The process is pinned to a fixed set of ``cores`` CPUs (the first of its
+    allowed set, as many as OMP_NUM_THREADS grants) and torch uses exactly
+    that many threads, so repetitions do not migrate or change width. For
+    every config, in a fixed order: the head count per repetition is fixed by
+    a probe so that one repetition takes about ``seconds`` (all heads if they
+    fit); one untimed repetition warms the allocator and caches, then whole
+    (b, h) heads are timed ``reps`` times, the same heads each time. Each
     repetition is extrapolated to the whole workload; the median and the
-    spread (min, max) over repetitions are reported."""
+    spread (max - min over the median) are reported."""
     import torch
     from custom_ops_amd.workloads import CONFIGS, make_inputs
     from oracle.oracle import oracle_fwd, torch_math_cpu
     try:
-        cores = len(os.sched_getaffinity(0))
+        allowed = sorted(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores) or cores))
+        allowed = list(range(os.cpu_count() or 1))
+    cores = min(len(allowed), int(os.environ.get("OMP_NUM_THREADS", len(allowed)) or len(allowed)))
+    try:
+        os.sched_setaffinity(0, allowed[:cores])
+    except (AttributeError, OSError):
+        pass
     torch.set_num_threads(cores)
     out = {}
     for name in ("cfg2", "cfg3", "cfg4", "cfg5", "cfg1"):
@@ -134,9 +144,10 @@ def cpu_baseline(seconds: float, reps: int = 3):
         torch_math_cpu(q, k, v, m, heads=heads[:2])           # probe
         per = max((time.perf_counter() - t0) / 2, 1e-6)
         n = max(1, min(len(heads), int(seconds / per)))
+        sel = heads[:n]
+        torch_math_cpu(q, k, v, m, heads=sel)                 # untimed repetition
         runs = []
         for r in range(reps):
-            sel = [heads[(r * n + i) % len(heads)] for i in range(n)]
             t0 = time.perf_counter()
             torch_math_cpu(q, k, v, m, heads=sel)
             runs.append((time.perf_counter() - t0) / n * len(heads) * 1e6)
@@ -163,9 +174,9 @@ def cpu_baseline(seconds: float, reps: int = 3):
         "cores": cores,
         "kind": "port",
         "sample": f"cfg2: {base['heads_per_rep']} whole (b,h) heads per repetition, median of "
-                  f"{reps} repetitions (spread {base['spread_pct']}%), fp32 torch math attention "
-                  f"(scores+mask, guarded softmax, P@V) on {_cpu_name()}, extrapolated to the "
-                  f"64 heads",
+                  f"{reps} repetitions after an untimed one (spread {base['spread_pct']}%), fp32 "
+                  f"torch math attention (scores+mask, guarded softmax, P@V) on {_cpu_name()}, "
+                  f"{cores} threads pinned to {cores} cores, extrapolated to the 64 heads",
         "us_full_workload": base["us"],
         "configs": out,
     }

@@ -34,7 +34,20 @@ EXPORTED = (
     "mi355_fa_abi_version",
     "mi355_fa_build_info",
 )
-ABI_VERSION = 1
+ABI_VERSION = 2
+
+
+class Variant(ctypes.Structure):
+    """Mirror of ``mi355_fa_variant`` (include/mi355_fa.h): kernel-variant
+    selection for parity tests and tuning. Every field 0 = the library's plan;
+    see the header for the meaning of each value."""
+
+    _fields_ = [(name, ctypes.c_int32) for name in
+                ("waves", "pack", "order", "loop", "fuse", "live", "deep", "mask_mfma")]
+
+    def __repr__(self) -> str:
+        set_ = {n: getattr(self, n) for n, _ in self._fields_ if getattr(self, n)}
+        return f"Variant({', '.join(f'{k}={v}' for k, v in set_.items())})"
 
 
 class Params(ctypes.Structure):
@@ -64,6 +77,7 @@ class Params(ctypes.Structure):
         ("num_splits", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("variant", ctypes.POINTER(Variant)),
     ]
 
 

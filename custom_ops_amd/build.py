@@ -83,23 +83,6 @@ def compile_checked(out_path: str, flags=None, verbose: bool = False) -> str:
     return out_path
 
 
-PROBE_SRC = os.path.join(PKG_DIR, "csrc", "hbm_probe.hip")
-PROBE_PATH = os.path.join(PKG_DIR, "libmi355_probe.so")
-
-
-def build_probe(verbose: bool = False) -> str:
-    """Compile the HBM read probe (measurement tooling for profiles/, a library
-    of its own: nothing of the operator loads it)."""
-    cmd = [hipcc(), *HIPCC_FLAGS, PROBE_SRC, "-o", PROBE_PATH + ".tmp"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
-    os.replace(PROBE_PATH + ".tmp", PROBE_PATH)
-    return PROBE_PATH
-
-
 TORCH_BINDING_SRC = os.path.join(PKG_DIR, "csrc", "torch_binding.cpp")
 TORCH_BINDING_PATH = os.path.join(PKG_DIR, "libmi355_fa_torch.so")
 
@@ -128,9 +111,8 @@ def build_torch_binding(verbose: bool = False) -> str:
 
 
 def build(verbose: bool = False) -> str:
-    """Compile the library (always recompiles), the C++ torch binding over it
-    and the measurement probe; return the library's path."""
-    build_probe(verbose=verbose)
+    """Compile the library (always recompiles) and the C++ torch binding over
+    it; return the library's path."""
     out = compile_checked(LIB_PATH, verbose=verbose)
     build_torch_binding(verbose=verbose)
     return out

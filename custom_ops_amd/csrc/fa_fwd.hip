@@ -58,6 +58,7 @@
 #include <type_traits>
 
 #include "mi355_fa.h"
+#include "bits.h"
 
 namespace mi355fa {
 
@@ -363,9 +364,9 @@ typedef const KParams CKParams;
 // the compiler thinks divergent
 __device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo),
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(low_u32(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(high_u32(a));
+  return make_rsrc(reinterpret_cast<const void*>(compose_u64(lo, hi)),
                    __builtin_amdgcn_readfirstlane(bytes));
 }
 __device__ __forceinline__ CKParams& kernarg_params(const KParams& pk) {
@@ -655,6 +656,44 @@ __device__ __forceinline__ void write_rows(const KParams& p, const f32x16 (&oacc
   }
 }
 
+// Memory ordering of the fused split tail (why the last arrival reads every
+// split's finished partials, with no fence instruction on either side):
+//   * Producer: each wave stores its partial O rows and LSEs with sc1 buffer
+//     stores. sc1 is exactly what the compiler emits for an agent-scope
+//     relaxed atomic store on gfx950 (global_store ... sc1): the store is
+//     written through this XCD's L2 to the level every XCD reads from.
+//     wait_vmcnt<0>() then blocks the wave until every one of its stores has
+//     been acknowledged (on gfx9 vmcnt counts stores until they complete), and
+//     wg_barrier() holds thread 0 until every wave has passed that wait. Only
+//     then does thread 0 issue the ticket compare-and-swap.
+//   * The ticket word: all arrivals are agent-scope read-modify-writes of one
+//     address, so they are totally ordered; the arrival whose count completes
+//     the row block has read the value written by every earlier arrival's
+//     CAS, each of which was issued after its workgroup's stores completed.
+//   * Consumer: the other threads read the LDS flag after a barrier that
+//     follows the CAS's return, so no load of the tail issues before the CAS
+//     has returned (the GPU does not issue loads speculatively). Every load of
+//     shared data (partials, LSEs) is an sc1 buffer load, the instruction the
+//     compiler emits for an agent-scope relaxed atomic load: it is served
+//     from the device-coherent level, never from a stale line of this XCD's L2.
+//   * This is what the compiler's own agent-scope release / acquire lowering
+//     provides (buffer_wbl2 sc1 + s_waitcnt vmcnt(0) before the atomic,
+//     s_waitcnt vmcnt(0) + buffer_inv sc1 after it) without its whole-cache
+//     writeback and invalidate: those exist for plain stores left dirty in L2
+//     and plain loads that could hit stale lines, and no plain store or load
+//     touches the shared data here. (A release that did the writeback made
+//     cfg5 2x slower: every workgroup wrote back its XCD's whole L2.)
+//   * The compiler cannot move the stores below the wait or the CAS above the
+//     barrier: both helpers end in __atomic_signal_fence(seq_cst), a code
+//     motion barrier for memory operations, around side-effecting s_waitcnt /
+//     s_barrier builtins. tests/test_isa.py checks the result in the assembly
+//     of every split kernel: between its last partial store and the CAS sit
+//     s_waitcnt vmcnt(0) and s_barrier in that order, every store in that
+//     stretch and every buffer load after the CAS carries sc1.
+//   * The argument is about the hardware's order, not the C++ memory model,
+//     in which relaxed atomics create no happens-before: the guarantees above
+//     are those of the gfx950 instructions the checked assembly contains.
+//
 // Row-block ticket word: a 48-bit launch tag above a 16-bit arrival count.
 // A word holding another tag restarts at 1, so workspace memory left by an
 // earlier launch needs no clearing. A graph replays a captured launch with its
@@ -1851,26 +1890,22 @@ static int cost_model_splits(int total_mblocks, int nb, int block_m, int d, int 
   return best;
 }
 
-// Live-range narrowing (narrow_to_live): on for split launches and for the
-// compiled kernel, whose prologue wait covers the probe; off for unsplit
-// launches of the assembly loops, which wait for nothing before their loop, so
-// the probe's memory round trip would be exposed on every workgroup (dense
-// masks: +2 % on cfg2/cfg3). MI355_FA_LIVE=0 turns it off, =1 on everywhere.
-static int live_mode() {
-  static const int f = [] {
-    const char* e = getenv("MI355_FA_LIVE");
-    return (e && (e[0] == '0' || e[0] == '1')) ? e[0] - '0' : 2;
-  }();
-  return f;
+// The caller's variant selection (all zero: the library's own choices).
+static mi355_fa_variant variant_of(const mi355_fa_params* p) {
+  mi355_fa_variant v{};
+  if (p->variant) v = *p->variant;
+  return v;
 }
 
-// MI355_FA_FUSE=0 keeps the combine launch for every split plan (A/B runs)
-static bool fuse_enabled() {
-  static const bool f = [] {
-    const char* e = getenv("MI355_FA_FUSE");
-    return !(e && e[0] == '0');
+// MI355_FA_NUM_SPLITS, the one tuning override read from the environment:
+// read once per process, 0 when unset or not a positive number.
+static int env_num_splits() {
+  static const int n = [] {
+    const char* e = getenv("MI355_FA_NUM_SPLITS");
+    const int v = e ? atoi(e) : 0;
+    return v > 0 ? v : 0;
   }();
-  return f;
+  return n;
 }
 
 struct Plan {
@@ -1880,6 +1915,15 @@ struct Plan {
   size_t o_part_bytes, lse_bytes, ticket_bytes, ws_bytes;
   int fuse;   // split tail fused into the main kernel (no combine launch)
   int deep;   // 4 waves, at most one workgroup per CU: three K/V stages
+  // Generated-assembly loop form for d = 128 8-wave plans with aligned mask
+  // rows: 3 = ping-pong (bf16; fp16 runs the 32-row loop), 1 = 32-row loop,
+  // 2 = 64-row loop, 0 = the compiled kernel.
+  int loop;
+  // Live-range narrowing: 2 = the default policy (on for split launches and
+  // for the compiled kernel, off for unsplit launches of the assembly loops),
+  // 1 = on everywhere, 0 = off.
+  int live;
+  int mask_mfma_off;   // the compiled kernel widens bf16 masks on the VALU
 };
 
 // Tile plan: the workgroup size (4 or 8 waves) and split count with the
@@ -1915,20 +1959,19 @@ static float plan_cost(const PlanCost& c, int bh, int sq, int num_n, int d, int 
 // rows, so packing them makes the waves of one workgroup read the same mask
 // rows together. A power of two dividing H / Hk, at most 4 (the 4-wave
 // workgroups and the 64-row waves of the 4-wave assembly form hold 4 heads).
-static int pick_pack(const mi355_fa_params* p) {
+static int pick_pack(const mi355_fa_params* p, const mi355_fa_variant& v) {
   const int ratio = p->h / p->h_k;
   int want = 4;
-  const char* e = getenv("MI355_FA_PACK");   // tuning override: 1, 2 or 4
-  if (e && (atoi(e) == 1 || atoi(e) == 2 || atoi(e) == 4)) want = atoi(e);
+  if (v.pack == 1 || v.pack == 2 || v.pack == 4) want = v.pack;
   int pk = 1;
   while (pk * 2 <= want && ratio % (pk * 2) == 0) pk *= 2;
   return pk;
 }
 
-static int order_head_major(const mi355_fa_params* p, const Plan& pl, int cus) {
-  const char* o = getenv("MI355_FA_ORDER");   // tuning override: "h" or "m"
-  if (o && o[0] == 'h') return 1;
-  if (o && o[0] == 'm') return 0;
+static int order_head_major(const mi355_fa_params* p, const Plan& pl, int cus,
+                            const mi355_fa_variant& v) {
+  if (v.order == 1) return 1;
+  if (v.order == 2) return 0;
   const double R = (double)(cus / 8 > 0 ? cus / 8 : 1) * (pl.waves == 4 ? 2 : 1);   // workgroups per XCD round
   const double G = p->h / pl.pack;                                   // head groups (one K/V head each)
   const double M = ceil_div(p->seqlen_q, pl.block_m / pl.pack);      // m-blocks
@@ -1948,21 +1991,14 @@ static int order_head_major(const mi355_fa_params* p, const Plan& pl, int cus) {
 
 static Plan make_plan(const mi355_fa_params* p, int cus) {
   Plan pl{};
-  pl.pack = pick_pack(p);
+  const mi355_fa_variant v = variant_of(p);
+  pl.pack = pick_pack(p, v);
   pl.num_n = ceil_div(p->seqlen_k, kBN);
   const int bh = p->b * p->h;
-  int s_fixed = p->num_splits;
-  if (s_fixed <= 0) {
-    const char* env = getenv("MI355_FA_NUM_SPLITS");
-    if (env && atoi(env) > 0) s_fixed = atoi(env);
-  }
+  int s_fixed = p->num_splits > 0 ? p->num_splits : env_num_splits();
   if (s_fixed > kMaxSplits) s_fixed = kMaxSplits;
   if (s_fixed > pl.num_n) s_fixed = pl.num_n;
-  int w_fixed = 0;
-  {   // tuning override of the workgroup size (4 or 8 waves)
-    const char* w = getenv("MI355_FA_WAVES");
-    if (w && (atoi(w) == 4 || atoi(w) == 8)) w_fixed = atoi(w);
-  }
+  const int w_fixed = (v.waves == 4 || v.waves == 8) ? v.waves : 0;
   const PlanCost& cm = p->d == 64 ? kCostD64 : kCostD128;
   int max_s = pl.num_n / 4 > 1 ? pl.num_n / 4 : 1;
   if (max_s > kMaxSplits) max_s = kMaxSplits;
@@ -1986,7 +2022,7 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   // the reverse; take the order whose round fetches fewer bytes. (MHA with
   // long Sq: m-blocks fastest; GQA, whose packed head groups share K/V, and
   // short Sq: heads fastest.)
-  pl.head_major = order_head_major(p, pl, cus);
+  pl.head_major = order_head_major(p, pl, cus, v);
   pl.num_m = ceil_div(p->seqlen_q, pl.block_m / pl.pack);
   pl.n_per_split = (s > 1) ? ceil_div(pl.num_n, s) : pl.num_n;
   if (s > 1) {
@@ -2000,19 +2036,18 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
     // row); more splits keep the combine launch, whose work spreads over the
     // whole chip instead of falling on each row block's last split
     pl.fuse = s <= kFuseMaxSplits && pl.o_part_bytes < (1ull << 31) && pl.lse_bytes < (1ull << 31) &&
-              fuse_enabled();
+              v.fuse >= 0;
   }
   pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
   // A 4-wave grid that puts at most one workgroup on each CU takes a third K/V
   // stage (112 KiB of LDS at d = 128: one workgroup per CU; cfg4 cold -7 %).
   {
-    static const bool deep_on = [] {
-      const char* e = getenv("MI355_FA_DEEP");   // tuning override: 0 keeps two stages
-      return !(e && e[0] == '0');
-    }();
     const int64_t wgs = (int64_t)p->b * (p->h / pl.pack) * pl.num_m * s;
-    pl.deep = (pl.waves == 4 && wgs <= cus && deep_on) ? 1 : 0;
+    pl.deep = (pl.waves == 4 && wgs <= cus && v.deep >= 0) ? 1 : 0;
   }
+  pl.loop = v.loop < 0 ? 0 : (v.loop >= 1 && v.loop <= 3 ? v.loop : 3);
+  pl.live = v.live < 0 ? 0 : (v.live > 0 ? 1 : 2);
+  pl.mask_mfma_off = v.mask_mfma < 0 ? 1 : 0;
   return pl;
 }
 
@@ -2078,9 +2113,6 @@ static hipError_t launch_main(const KParams& kp, hipStream_t st) {
   return hipGetLastError();
 }
 
-// The generated-loop kernel serves the 8-wave plans at d = 128 with 16-byte
-// aligned mask rows. MI355_FA_ASM selects its form: 1 (default) = 8 waves of
-// 32 rows, 2 = 4 waves of 64 rows, 0 = the compiled 8-wave kernel instead.
 // A 48-bit launch tag, never 0, distinct for every launch of the process
 // (splitmix64 of a per-process random seed plus a launch counter): a ticket
 // word left by an earlier launch in reused workspace memory carries another
@@ -2100,32 +2132,22 @@ static unsigned long long next_launch_tag() {
   return z ? z : 1ull;
 }
 
-static int asm_form() {
-  static const int f = [] {
-    const char* e = getenv("MI355_FA_ASM");
-    // 3 (default): bf16 runs the ping-pong loop, fp16 the 32-row loop;
-    // 1: the 32-row loop for both; 2: the 64-row loop; 0: the compiled kernel
-    return (e && (e[0] >= '0' && e[0] <= '3')) ? e[0] - '0' : 3;
-  }();
-  return f;
-}
-
 // Whether a launch runs one of the generated-assembly loops (d = 128, 8-wave
 // plans, 16-byte aligned mask rows) rather than the compiled kernel.
 template <int D, bool BF16>
 static bool runs_asm_loop(const KParams& kp, const Plan& pl) {
   // bf16 adds the mask on the matrix core, which needs bf16(1/scale) > 1.0078
   // (-max_bf16 · (1/scale) must overflow to -inf): scale < 0.99
-  return D == 128 && pl.waves == 8 && kp.mask_direct && asm_form() && (!BF16 || kp.scale < 0.99f);
+  return D == 128 && pl.waves == 8 && kp.mask_direct && pl.loop && (!BF16 || kp.scale < 0.99f);
 }
 
 template <int D, bool BF16, bool SPLIT>
 static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t st) {
   if constexpr (D == 128) {
     if (runs_asm_loop<D, BF16>(kp, pl)) {
-      if (asm_form() == 3 && BF16)
+      if (pl.loop == 3 && BF16)
         hipLaunchKernelGGL((fa_fwd_kernel_pp<SPLIT>), dim3(kp.total), dim3(512), 0, st, kp);
-      else if (asm_form() == 2)
+      else if (pl.loop == 2)
         hipLaunchKernelGGL((fa_fwd_kernel_asm<2, BF16, SPLIT>), dim3(kp.total), dim3(256), 0, st, kp);
       else
         hipLaunchKernelGGL((fa_fwd_kernel_asm<1, BF16, SPLIT>), dim3(kp.total), dim3(512), 0, st, kp);
@@ -2139,7 +2161,7 @@ static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t 
 template <int D, bool BF16>
 static hipError_t launch(const KParams& kp_in, const CParams& cp, const Plan& pl, hipStream_t st) {
   KParams kp = kp_in;
-  const int lm = live_mode();
+  const int lm = pl.live;
   kp.live = pl.num_n >= 4 && (lm == 1 || (lm == 2 && (pl.splits > 1 || !runs_asm_loop<D, BF16>(kp, pl))));
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
   // the fused tail is in the compiled kernel only (the assembly loops keep no
@@ -2243,10 +2265,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.num_splits = pl.splits; kp.n_per_split = pl.n_per_split;
   kp.total = (int)total;
   kp.scale = p->scale_softmax;
-  {
-    const char* e = getenv("MI355_FA_MASK_MFMA");   // tuning override: 0 widens the mask on the VALU
-    kp.mask_mfma = (p->dtype == MI355_FA_BF16 && p->scale_softmax < 0.99f && !(e && e[0] == '0')) ? 1 : 0;
-  }
+  kp.mask_mfma = (p->dtype == MI355_FA_BF16 && p->scale_softmax < 0.99f && !pl.mask_mfma_off) ? 1 : 0;
   {
     const float c2 = p->scale_softmax * kLog2e, slack = kRescaleSlack / p->scale_softmax;
     memcpy(&kp.c2_bits, &c2, 4);

@@ -47,15 +47,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "fa_loop.inc")
-# Timing-only ablations (never used for the committed output): comma list of
-# noexp, novaluy, noqk, nopv, nodmam, nobar, nodma, nolds, ts (phase
-# timestamps into a debug buffer whose address the scratch build binds to
-# v[231:232])
-ABL = set(filter(None, os.environ.get("W64_ABLATE", "").split(",")))
-BAL = "nobal" not in ABL             # 64-row bf16 loop: cost-balanced tile body
-BAL_BUDGET = next((int(a[3:]) for a in ABL if a.startswith("bud")), 28)   # VALU cycles per MFMA
-FP32_SUM = "dotsum" not in ABL       # row sums by v_add over fp32 P (dotsum: by v_dot2)
-PRIO_STEPS = next((int(a[4:]) for a in ABL if a.startswith("prio")), 0)
+BAL_BUDGET = 28        # 64-row bf16 loop: VALU cycles per MFMA in the cost-balanced tile body
 
 D = 128
 KD = D // 16          # 16-d steps of QK
@@ -80,7 +72,7 @@ def configure(nh):
     r = 2 * SBUF
     g["KWIN"] = r; r += 16               # K operand window, 4 slots
     g["VWIN"] = r; r += 16               # V operand window, 4 slots
-    g["MWIN"] = r; r += 32 if (nh == 2 and BAL) else 8   # mask window, slots of 4
+    g["MWIN"] = r; r += 32 if nh == 2 else 8   # mask window, slots of 4
     g["MSEL"] = r; r += 8                # bf16 mask selectors A_0, A_1
     g["NKL"] = 16 // WAVES               # K (and V) DMA loads per wave per tile
     g["NML"] = 4 * nh                    # mask DMA loads per wave per tile
@@ -107,7 +99,7 @@ def configure(nh):
     g["TAL"], g["WT1"] = T + 2 + 3 * nh, T + 3 + 3 * nh
     # bf16 mask chunks in flight: the mask window plus (idle during PV) K window
     g["MSLOTS"] = [MWIN, MWIN + 4, KWIN, KWIN + 4, KWIN + 8, KWIN + 12][:6 if nh == 2 else 4]
-    if nh == 2 and BAL:     # the balanced body: one slot per chunk (the K window is busy)
+    if nh == 2:     # the balanced body: one slot per chunk (the K window is busy)
         g["MSLOTS"] = [MWIN + 4 * i for i in range(8)]
     g["NSLOT"] = len(MSLOTS)
 
@@ -213,9 +205,6 @@ class Phase:
         -1 = before the first MFMA) and goes exactly there; others_span: the
         scalar/DMA items spread over the first that many MFMAs only."""
         st = self.st
-        if "nolds" in ABL:
-            mfmas = [dict(m, needs=[]) for m in mfmas]
-            valus = [dict(v, needs=[]) for v in valus]
         prog = []
         valus, others = list(valus), list(others)
         nm = len(mfmas)
@@ -480,18 +469,6 @@ def exp_valus(bf16, s_cur, fp32_sum=False):
     return out
 
 
-def rowsum_valus(bf16, s_cur):
-    one = "0x3f803f80" if bf16 else "0x3c003c00"
-    op = "v_dot2c_f32_bf16" if bf16 else "v_dot2c_f32_f16"
-    out = []
-    for k in range(16):
-        for h in range(NH):
-            base = S(s_cur, h, 0, 0)
-            out.append(valu(f"{op} v{LSUM + h}, {one}, v{base + k}", [base + k, LSUM + h], [LSUM + h],
-                            kind="dot"))
-    return out
-
-
 def mask_add_valus(bf16, s_next, mstage_off):
     """u += mask·(1/scale) for the next tile, both halves. The 16 mask values of
     (half h, block b) are two 16-byte LDS reads into a window slot of 8."""
@@ -741,8 +718,6 @@ def gen(bf16: bool, nh: int = 2) -> str:
         for i, nm in enumerate(names):
             st.emit(f"s_mov_b32 s{base + i}, %[{nm}]")
     st.emit("s_mov_b32 s92, %[ntiles]")          # tiles left to score, including the next one
-    if "ts" in ABL:
-        st.emit("s_mov_b64 s[96:97], %[dbgp]")
     st.nop(4)
     st.ready.clear()
 
@@ -763,64 +738,26 @@ def gen(bf16: bool, nh: int = 2) -> str:
         st.emit(line)
     st.ready.clear()
 
-    def stamp(k):
-        if "ts" not in ABL:
-            return
-        # the V window is idle at every stamp point; the pointer lives in s[96:97]
-        for line in ["s_memtime s[98:99]", "s_waitcnt lgkmcnt(0)", f"v_mov_b32 v{VWIN}, s98",
-                     f"v_mov_b32 v{VWIN + 1}, s99", f"v_mov_b32 v{VWIN + 2}, 0",
-                     f"global_store_dwordx2 v{VWIN + 2}, v[{VWIN}:{VWIN + 1}], s[96:97] offset:{8 * k}"]:
-            st.emit(line)
-        if k == 3:
-            st.emit("s_add_u32 s96, s96, 32")
-            st.emit("s_addc_u32 s97, s97, 0")
-
-    def prio_steps(start, nm):
-        # Two waves share each SIMD and the older one wins issue ties, so it
-        # finishes its tile early and idles at the barrier while the younger
-        # one runs alone. The priority drops as a wave gets through its
-        # MFMAs, so the wave that is behind gets the issue slots.
-        steps = PRIO_STEPS
-        if not steps:
-            return
-        marks = {round(nm * (k + 1) / steps): steps - 1 - k for k in range(steps - 1)}
-        out, seen = [], 0
-        for line in st.lines[start:]:
-            out.append(line)
-            if line.startswith("v_mfma"):
-                seen += 1
-                if seen in marks:
-                    out.append(f"s_setprio {marks[seen]}")
-        st.lines[start:] = out
-
     def body(p, last):
         nxt = 1 - p
         lab = f"{L}_b{p}{'L' if last else ''}"
-        if "nobar" not in ABL:
-            st.emit("s_waitcnt vmcnt(0) lgkmcnt(0)")
-            st.emit("s_barrier")
-        else:
-            st.emit("s_waitcnt lgkmcnt(0)")
-        if PRIO_STEPS:
-            st.emit(f"s_setprio {PRIO_STEPS - 1}")
-        stamp(0)
+        st.emit("s_waitcnt vmcnt(0) lgkmcnt(0)")
+        st.emit("s_barrier")
         if last:
-            Phase(st).run([], exp_only_valus(p, fp32_sum=FP32_SUM))
-            Phase(st).run(pv_mfmas(bf16, V_LDS + p * KSTAGE, p),
-                          cvt_valus(bf16, p) + ([] if FP32_SUM else rowsum_valus(bf16, p)))
+            Phase(st).run([], exp_only_valus(p, fp32_sum=True))
+            Phase(st).run(pv_mfmas(bf16, V_LDS + p * KSTAGE, p), cvt_valus(bf16, p))
             return
         # tile n+2's K and mask into stage p (out of range past the last tile),
         # tile n+1's V into stage 1-p: single instructions spread over the tile
-        others = [] if "nodma" in ABL else dma_items(p, nxt, p, True, True, "nodmam" not in ABL)
+        others = dma_items(p, nxt, p, True, True, True)
         # One stream per tile: QK(n+1) then PV(n) (with the bf16 mask MFMAs of
         # n+1 between the first PV MFMAs) on the matrix core; exp(n), cvt(n),
         # clamps, row sums, tail and max of n+1 on the VALU. One load queue,
         # so V and mask reads of PV prefetch under the end of QK.
-        qk = [] if "noqk" in ABL else qk_mfmas(bf16, K_LDS + nxt * KSTAGE, nxt)
-        pv = [] if "nopv" in ABL else pv_mfmas(bf16, V_LDS + p * KSTAGE, p)
-        ex = [] if "noexp" in ABL else exp_only_valus(p, fp32_sum=FP32_SUM)
-        rs = [] if FP32_SUM else rowsum_valus(bf16, p)
-        if bf16 and NH == 2 and BAL:
+        qk = qk_mfmas(bf16, K_LDS + nxt * KSTAGE, nxt)
+        pv = pv_mfmas(bf16, V_LDS + p * KSTAGE, p)
+        ex = exp_only_valus(p, fp32_sum=True)
+        if bf16 and NH == 2:
             balanced_body(st, qk, pv, ex, others, nxt, lab)
             return
         if bf16:
@@ -841,25 +778,18 @@ def gen(bf16: bool, nh: int = 2) -> str:
             late = [tail_item(f"{lab}_t", nxt, left=2)] + max_valus(nxt)
             for it in late:
                 it["min_mfma"] = mpos[-1]
-            vy = interleave(cvt_valus(bf16, p), clamps) + rs + late
+            vy = interleave(cvt_valus(bf16, p), clamps) + late
         else:
             mf = qk + pv
             late = mask_add_valus(bf16, nxt, M_LDS + nxt * MSTAGE) + \
                 [tail_item(f"{lab}_t", nxt, left=2)] + max_valus(nxt)
             for it in late:     # they read the QK results: after the last QK MFMA
                 it["min_mfma"] = len(qk) - 1
-            vy = cvt_valus(bf16, p) + rs + late
-        if "novaluy" in ABL:
-            vy = [{"kind": "raw", "lines": ["s_mov_b64 s[94:95], 0"]}]
-        start = len(st.lines)
-        Phase(st).run(mf, ex + vy, others, valu_lead=0 if "noexp" in ABL else 8)
-        prio_steps(start, len(mf))
+            vy = cvt_valus(bf16, p) + late
+        Phase(st).run(mf, ex + vy, others, valu_lead=8)
         st.emit("s_sub_u32 s92, s92, 1")
-        stamp(1)
-        stamp(2)
         for line in rescale_lines(f"{lab}_r"):
             st.emit(line)
-        stamp(3)
         st.ready.clear()
 
     def balanced_body(st, qk, pv, ex, others, nxt, lab):
@@ -887,17 +817,10 @@ def gen(bf16: bool, nh: int = 2) -> str:
         for it in late:
             it["earliest"] = 40
         vy = plan_slots(len(mf), [clamps, chain, late], BAL_BUDGET)
-        if "novaluy" in ABL:
-            vy = [{"kind": "raw", "lines": ["s_mov_b64 s[94:95], 0"]}]
-        start = len(st.lines)
         Phase(st).run(mf, vy, others, exact=True, others_span=36)
-        prio_steps(start, len(mf))
         st.emit("s_sub_u32 s92, s92, 1")
-        stamp(1)
-        stamp(2)
         for line in rescale_lines(f"{lab}_r"):
             st.emit(line)
-        stamp(3)
         st.ready.clear()
 
     st.emit(f"{L}_loop:")
@@ -914,8 +837,6 @@ def gen(bf16: bool, nh: int = 2) -> str:
     st.emit(f"{L}_last1:")
     body(1, True)
     st.emit(f"{L}_end:")
-    if PRIO_STEPS:
-        st.emit("s_setprio 0")
     # O out of the AGPRs once the last PV MFMA has finished
     st.nop(16)
     for r in range(64 * NH):
@@ -940,10 +861,10 @@ PP_MST = 32768
 PP_VBASE = 3 * PP_KST
 PP_MBASE = 6 * PP_KST
 PP_LDS = PP_MBASE + 2 * PP_MST      # 160 KiB
-PP_KSLOTS = next((int(a[2:]) for a in ABL if a.startswith("ks")), 6)   # K operand window slots
-PP_VSLOTS = next((int(a[2:]) for a in ABL if a.startswith("vs")), 6)   # V (and mask) window slots
-PP_MAXQ = next((int(a[1:]) for a in ABL if a[:1] == "q" and a[1:].isdigit()), 12)   # LDS reads in flight
-PP_KPRE = next((int(a[4:]) for a in ABL if a.startswith("kpre")), 6)   # K operands read in the V phase before
+PP_KSLOTS = 6         # K operand window slots
+PP_VSLOTS = 6         # V (and mask) window slots
+PP_MAXQ = 12          # LDS reads in flight
+PP_KPRE = 6           # K operands read in the V phase before
 PP_DK = (0, 8, 32, 40)               # key offset of K DMA load i (16 rows on, π-permuted)
 
 
@@ -988,9 +909,7 @@ def pp_qk_mfmas(kstage, sbuf):
             ld = Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(K_RD + kd)} offset:{off}", vrange(w, 4),
                       pre=k < PP_KPRE)
             dst = S(sbuf, 0, kb, 0)
-            if "ppnokr" in ABL:   # timing only: no K reads, the A operand real (V window) data
-                w = VWIN + 4 * (k % PP_VSLOTS)
-            out.append({"kind": "mfma", "needs": [] if ("ppnok" in ABL or "ppnokr" in ABL) else [ld],
+            out.append({"kind": "mfma", "needs": [ld],
                         "text": f"v_mfma_f32_32x32x16_bf16 {vreg(dst, 16)}, {vreg(w, 4)}, "
                                 f"{areg(QA + 4 * kd, 4)}, {vreg(dst, 16)}",
                         "dst": vrange(dst, 16), "src": vrange(w, 4) + vrange(dst, 16)})
@@ -1006,15 +925,8 @@ def pp_k_preread(kstage):
         w = KWIN + 4 * (k % PP_KSLOTS)
         off = kstage * PP_KST + kb * 32 * D * 2
         loads.append(Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(K_RD + kd)} offset:{off}", vrange(w, 4)))
-    return {"kind": "raw", "lines": [], "needs": [] if ("ppnok" in ABL or "ppnokr" in ABL) else loads}
+    return {"kind": "raw", "lines": [], "needs": loads}
 
-
-# experiment: the P conversion and row sum of tile t in the M phase of tile
-# t+1 (slower: the M phase lengthens by more than the V phase shortens)
-P_IN_M = "ppinm" in ABL
-
-# experiment: a tile's DMA issued from the V phase after its M phase
-DMA_IN_V = "ppdmav" in ABL
 
 PP_MCHUNKS = [(0, 0), (1, 0), (0, 1), (1, 1)]   # (block b, chunk c), issue order
 
@@ -1045,29 +957,8 @@ def pp_mask_mfmas(sbuf):
     return out
 
 
-def pp_p_valus(sbuf):
-    """The P of the previous tile, left in fp32 by its V phase, summed into the
-    row sum and rounded to bf16 pairs in place (key step j lands in
-    S(sbuf) + 4j .. +3, tagged cvt{j} for its PV MFMAs). Runs in the M phase,
-    under this wave's own MFMAs, off the V phase that bounds the tile."""
-    out = []
-    base = S(sbuf, 0, 0, 0)
-    for grp in range(4):
-        regs = [base + 8 * grp + e for e in range(8)]
-        for r in regs:
-            out.append(valu(f"v_add_f32 v{LSUM}, v{LSUM}, v{r}", [r, LSUM], [LSUM]))
-        for k in range(4):
-            a, b = regs[2 * k], regs[2 * k + 1]
-            it = valu(f"v_cvt_pk_bf16_f32 v{base + 4 * grp + k}, v{a}, v{b}", [a, b], [base + 4 * grp + k])
-            it["tag"] = f"cvt{grp}"
-            out.append(it)
-    return out
-
-
-def pp_pv_mfmas(vstage, sbuf, p_here=False):
-    """16 MFMAs of Oᵀ += Vᵀ·Pᵀ, transposed V operands through the V window
-    (p_here: key step j's P is converted in this phase, by the items tagged
-    cvt{j})."""
+def pp_pv_mfmas(vstage, sbuf):
+    """16 MFMAs of Oᵀ += Vᵀ·Pᵀ, transposed V operands through the V window."""
     out = []
     k = 0
     for j in range(4):
@@ -1079,10 +970,6 @@ def pp_pv_mfmas(vstage, sbuf, p_here=False):
             l1 = Load(f"ds_read_b64_tr_b16 {vreg(w + 2, 2)}, {vreg(V_RD + db)} offset:{off + 4 * D * 2}",
                       vrange(w + 2, 2))
             nd = [l0, l1]
-            if "ppvb128" in ABL:    # timing only: one plain 16-byte read instead of two transposing ones
-                nd = [Load(f"ds_read_b128 {vreg(w, 4)}, {vreg(V_RD + db)} offset:{off}", vrange(w, 4))]
-            if "ppnov" in ABL:      # timing only: no V operand reads
-                nd = []
             k += 1
             pr = S(sbuf, 0, 0, 0) + 4 * j
             o = OA + 16 * db
@@ -1090,8 +977,6 @@ def pp_pv_mfmas(vstage, sbuf, p_here=False):
                         "text": f"v_mfma_f32_32x32x16_bf16 {areg(o, 16)}, {vreg(w, 4)}, {vreg(pr, 4)}, "
                                 f"{areg(o, 16)}",
                         "dst": [], "src": vrange(w, 4) + vrange(pr, 4)})
-            if p_here:
-                out[-1]["deps"] = (f"cvt{j}",)
     return out
 
 
@@ -1118,20 +1003,18 @@ def pp_dma_items(t_plus2_kstage, t_plus1_vstage, mstage, group_a, parts="kvm"):
 
     # loads 2 and 3 of each tensor use its second descriptor (s68 K, s72 V,
     # s76 mask), whose base is 32 keys / 32 rows / 16 mask rows on
-    kv_a = "ppkva" in ABL       # experiment: group A issues V as well
-    if "ppnokv" not in ABL:     # (ppnokv: timing only, no K/V DMA)
-        if "k" in parts and group_a:
-            for i in range(4):
-                load(80 if i < 2 else 68, "lds_k", t_plus2_kstage * PP_KST + i * 4096, K_OFF + i % 2)
-            adv(80, "%[kstep]")
-            adv(68, "%[kstep]")
-        if "v" in parts and group_a == kv_a:
-            for i in range(4):
-                load(84 if i < 2 else 72, "lds_v", PP_VBASE + t_plus1_vstage * PP_KST + i * 4096,
-                     V_OFF + i % 2)
-            adv(84, "%[vstep]")
-            adv(72, "%[vstep]")
-    if "ppnomdma" in ABL or "ppnomask" in ABL or "m" not in parts:   # (timing only: no mask DMA)
+    if "k" in parts and group_a:
+        for i in range(4):
+            load(80 if i < 2 else 68, "lds_k", t_plus2_kstage * PP_KST + i * 4096, K_OFF + i % 2)
+        adv(80, "%[kstep]")
+        adv(68, "%[kstep]")
+    if "v" in parts and not group_a:
+        for i in range(4):
+            load(84 if i < 2 else 72, "lds_v", PP_VBASE + t_plus1_vstage * PP_KST + i * 4096,
+                 V_OFF + i % 2)
+        adv(84, "%[vstep]")
+        adv(72, "%[vstep]")
+    if "m" not in parts:
         return items, n
     for i in range(4):
         load(88 if i < 2 else 76, "lds_m", mstage * PP_MST + i * 1024, M_OFF + i % 2)
@@ -1208,20 +1091,6 @@ def pp_group(group_a, L):
     passes one extra barrier first, A one extra at the end."""
     st = Stream()
 
-    def stamp(k):
-        # timing builds: s_memtime into the debug buffer (4 stamps per tile)
-        if "ppts" not in ABL:
-            return
-        for line in ["s_memtime s[98:99]", "s_waitcnt lgkmcnt(0)", f"v_mov_b32 v{TSW}, s98",
-                     f"v_mov_b32 v{TTH}, s99", f"v_mov_b32 v{TAL}, 0",
-                     f"global_store_dwordx2 v{TAL}, v[{TSW}:{TTH}], s[96:97] offset:{8 * k}"]:
-            st.emit(line)
-        if k == 3:
-            st.emit("s_add_u32 s96, s96, 32")
-            st.emit("s_addc_u32 s97, s97, 0")
-
-    if "ppts" in ABL:
-        st.emit("s_mov_b64 s[96:97], %[dbgp]")
     if not group_a:
         st.emit("s_barrier")
     # operands of M_0: mask(0) clamped, K(0)'s first operands
@@ -1229,24 +1098,15 @@ def pp_group(group_a, L):
 
     def m_phase(t, first, last, prev_batch):
         """M_t; t is the tile index mod 6 (stages and buffers)."""
-        stamp(0)
         mf = [] if last else pp_mask_mfmas(t % 2) + pp_qk_mfmas(t % 3, t % 2)
-        pv = []
         if not first:
-            mf += pp_pv_mfmas((t - 1) % 3, (t - 1) % 2, p_here=P_IN_M)
-            if P_IN_M:
-                pv = pp_p_valus((t - 1) % 2)
+            mf += pp_pv_mfmas((t - 1) % 3, (t - 1) % 2)
         items, n = ([], 0) if last else pp_dma_items((t + 2) % 3, (t + 1) % 3, t % 2, group_a)
-        if DMA_IN_V:             # this tile's DMA goes out in the V phase after
-            items, n = [], 0
-        if "ppnomf" in ABL:      # timing only: no MFMAs (the DMA still runs)
-            mf = []
-        Phase(st, PP_MAXQ).run(mf, pv, items)
+        Phase(st, PP_MAXQ).run(mf, [], items)
         # the batch of the previous M phase has landed (LDS DMA: visible to
         # the other waves after the barrier)
         if prev_batch is not None:
             st.emit(f"s_waitcnt vmcnt({n})")
-        stamp(1)
         if not (last and not group_a):
             st.emit("s_barrier")
         return n
@@ -1254,23 +1114,10 @@ def pp_group(group_a, L):
     def v_phase(t, lab, last=False):
         vy = [tail_item(f"{lab}_t", t % 2, left=0)] + max_valus(t % 2)
         vy.append({"kind": "raw", "lines": rescale_lines(f"{lab}_r")})
-        if P_IN_M:               # P stays fp32 until the next M phase
-            vy += exp_only_valus(t % 2)
-        elif "ppdot" in ABL:     # row sum by v_dot2 over the bf16 P
-            vy += exp_valus(True, t % 2) + rowsum_valus(True, t % 2)
-        else:
-            vy += exp_valus(True, t % 2, fp32_sum=True)
-        if "ppnovalu" in ABL:    # timing only: the V phase keeps only its reads
-            vy = []
-        if "ppnomask" not in ABL:   # (ppnomask: timing only, no mask reads)
-            vy += pp_mask_preread((t + 1) % 2)
+        vy += exp_valus(True, t % 2, fp32_sum=True)
+        vy += pp_mask_preread((t + 1) % 2)
         vy += [pp_k_preread((t + 1) % 3)]
-        if DMA_IN_V and not last:
-            dma, _ = pp_dma_items((t + 2) % 3, (t + 1) % 3, t % 2, group_a)
-            vy = interleave(vy, dma)
-        stamp(2)
         Phase(st, PP_MAXQ).run([], vy)
-        stamp(3)
         st.emit("s_barrier")
 
     m_phase(0, True, False, None)
@@ -1306,8 +1153,6 @@ def operand_macros_pp():
            f'"{{{vreg(M_RD, 4)}}}"(mrd)', f'"{{{vreg(MSEL, 8)}}}"(msel)']
     ins += [f'[{n}] "s"({n})' for n in ("mclamp", "c2", "slack", "neginf", "lim", "lds_k", "lds_v", "lds_m",
                                          "kstep", "vstep", "ntiles", "grp")]
-    if "ppts" in ABL:
-        ins.append('[dbgp] "s"(dbgp)')
     clob = list(range(KWIN, MSEL)) + [MLOG] + [r for r in range(T, NVGPR) if r != TAL]
     cl = [f'"v{r}"' for r in clob] + [f'"a{r}"' for r in range(NAGPR)]
     cl += [f'"s{r}"' for r in range(96, 100)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
@@ -1336,9 +1181,6 @@ def operand_macros(prefix, bf16):
     clob += [MLOG + h for h in range(NH)] + list(range(T, FIN))
     cl = [f'"v{r}"' for r in clob] + [f'"a{r}"' for r in range(NAGPR)]
     cl += [f'"s{r}"' for r in range(80, 98)] + ['"m0"', '"vcc"', '"scc"', '"memory"']
-    if "ts" in ABL:     # timing-only scratch builds: the timestamp pointer (SGPR pair)
-        ins.append('[dbgp] "s"(dbgp)')
-        cl += ['"s98"', '"s99"']
     dt = "BF16" if bf16 else "F16"
     return [f"#define {prefix}_OUTPUTS_{dt} " + ", ".join(outs),
             f"#define {prefix}_INPUTS_{dt} " + ", ".join(ins),

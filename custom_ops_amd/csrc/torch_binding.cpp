@@ -8,10 +8,14 @@
 // the same operator through torch.library instead, so a process uses one or
 // the other.
 //
-// Argument checks: the tensor properties the C ABI cannot see (device, rank,
-// dtype agreement, innermost stride); shapes, GQA divisibility, alignment and
-// the mask extent are checked by mi355_fa_fwd itself, whose error text is
-// raised unchanged.
+// Argument checks: the reference operator's checks, in its order and with its
+// messages (csrc/fa/fa_fwd_op.cu:53-108), so callers see the same
+// RuntimeError text through either binding. Two checks the reference does not
+// make come after the ones it shares: all inputs on q's GPU, and k/v head
+// counts equal (the C ABI carries one Hk, so a v with other heads would be
+// read out of range). Everything shape-related is settled here, before any
+// pointer reaches the library; mi355_fa_fwd then checks alignment and the
+// 32-bit range limits of its buffer addressing.
 // PyTorch-ROCm presents GPUs as the "cuda" device type: the guard and the
 // stream are the HIP ones that accept it (the *MasqueradingAsCUDA classes)
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
@@ -27,18 +31,46 @@ namespace {
 
 at::Tensor mha_fwd_with_mask_mi355(const at::Tensor& q, const at::Tensor& k,
                                       const at::Tensor& v, const at::Tensor& mask) {
-  for (const at::Tensor* t : {&q, &k, &v, &mask}) {
-    TORCH_CHECK(t->is_cuda() && t->device() == q.device(), "all inputs must be on the same GPU");
-    TORCH_CHECK(t->dim() == 4, "q, k, v and mask must be 4-D");
-    TORCH_CHECK(t->scalar_type() == q.scalar_type(), "q, k, v and mask must share one dtype");
-  }
-  TORCH_CHECK(q.scalar_type() == at::kBFloat16 || q.scalar_type() == at::kHalf,
-              "q must be float16 or bfloat16");
-  TORCH_CHECK(q.stride(3) == 1 && k.stride(3) == 1 && v.stride(3) == 1 && mask.stride(3) == 1,
-              "the last dimension of q, k, v and mask must be contiguous");
-  TORCH_CHECK(mask.size(0) == q.size(0) && mask.size(1) == 1, "mask must be (B, 1, >=Sq, >=Sk)");
+  TORCH_CHECK(q.is_cuda(), "q must be a CUDA tensor");
+  TORCH_CHECK(k.is_cuda(), "k must be a CUDA tensor");
+  TORCH_CHECK(v.is_cuda(), "v must be a CUDA tensor");
+  TORCH_CHECK(mask.is_cuda(), "mask must be a CUDA tensor");
+
+  const bool is_fp16 = q.scalar_type() == at::kHalf;
+  const bool is_bf16 = q.scalar_type() == at::kBFloat16;
+  TORCH_CHECK(is_fp16 || is_bf16, "q must be float16 or bfloat16");
+  TORCH_CHECK(k.scalar_type() == q.scalar_type(), "k dtype must match q");
+  TORCH_CHECK(v.scalar_type() == q.scalar_type(), "v dtype must match q");
+  TORCH_CHECK(mask.scalar_type() == q.scalar_type(), "mask dtype must match q");
+
+  TORCH_CHECK(q.is_contiguous(), "q must be contiguous");
+  TORCH_CHECK(k.is_contiguous(), "k must be contiguous");
+  TORCH_CHECK(v.is_contiguous(), "v must be contiguous");
+  TORCH_CHECK(mask.is_contiguous(), "mask must be contiguous");
+
+  TORCH_CHECK(q.dim() == 4, "q must be 4D (B, H, Sq, d)");
+  TORCH_CHECK(k.dim() == 4, "k must be 4D (B, Hk, Sk, d)");
+  TORCH_CHECK(v.dim() == 4, "v must be 4D (B, Hk, Sk, d)");
+  TORCH_CHECK(mask.dim() == 4, "mask must be 4D (B, 1, Sq, Sk)");
+
+  const int64_t B = q.size(0), H = q.size(1), Sq = q.size(2), d = q.size(3);
+  const int64_t Hk = k.size(1), Sk = k.size(2);
+  TORCH_CHECK(k.size(0) == B && v.size(0) == B && mask.size(0) == B, "Batch size mismatch");
+  TORCH_CHECK(k.size(3) == d && v.size(3) == d, "head_dim mismatch between q/k/v");
+  TORCH_CHECK(k.size(2) == Sk && v.size(2) == Sk, "seqlen_k mismatch between k/v");
+  TORCH_CHECK(Hk > 0 && H % Hk == 0, "n_heads must be divisible by n_kv_heads (GQA)");
+  TORCH_CHECK(d == 64 || d == 128, "Only head_dim=64 or head_dim=128 is supported");
+  TORCH_CHECK(mask.size(1) == 1 && mask.size(2) >= Sq && mask.size(3) >= Sk,
+              "mask shape must be (B, 1, >=Sq, k-dim >= Sk)");
+
+  // not in the reference (see the note at the top of this file)
+  TORCH_CHECK(k.device() == q.device() && v.device() == q.device() && mask.device() == q.device(),
+              "q, k, v and mask must be on the same device");
+  TORCH_CHECK(v.size(1) == Hk, "n_kv_heads mismatch between k/v");
+
   c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  auto out = at::empty_like(q, q.options().memory_format(at::MemoryFormat::Contiguous));
+  auto out = at::empty_like(q);
+  if (out.numel() == 0) return out;
   mi355_fa_params p{};
   p.q = q.data_ptr(); p.k = k.data_ptr(); p.v = v.data_ptr(); p.mask = mask.data_ptr();
   p.o = out.data_ptr();

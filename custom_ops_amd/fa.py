@@ -17,8 +17,8 @@ come from the caching allocator as one workspace tensor sized by the library.
 """
 from __future__ import annotations
 
+import ctypes
 import math
-import os
 
 import torch
 
@@ -59,15 +59,15 @@ def _valid(q, k, v, mask) -> bool:
 
 
 def validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor) -> None:
-    """Input contract, in the reference's order (csrc/fa/fa_fwd_op.cu:53-108)."""
+    """Input contract, in the reference's order and with its messages
+    (csrc/fa/fa_fwd_op.cu:53-108), then two checks of this build's own. The
+    C++ binding (csrc/torch_binding.cpp) makes the same checks in the same order."""
     if _valid(q, k, v, mask):
         return
     _check(q.is_cuda, "q must be a CUDA tensor")
     _check(k.is_cuda, "k must be a CUDA tensor")
     _check(v.is_cuda, "v must be a CUDA tensor")
     _check(mask.is_cuda, "mask must be a CUDA tensor")
-    _check(k.device == q.device and v.device == q.device and mask.device == q.device,
-           "q, k, v and mask must be on the same device")
 
     is_fp16 = q.dtype == torch.float16
     is_bf16 = q.dtype == torch.bfloat16
@@ -91,37 +91,48 @@ def validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tens
     _check(k.shape[0] == B and v.shape[0] == B and mask.shape[0] == B, "Batch size mismatch")
     _check(k.shape[3] == d and v.shape[3] == d, "head_dim mismatch between q/k/v")
     _check(k.shape[2] == Sk and v.shape[2] == Sk, "seqlen_k mismatch between k/v")
-    _check(v.shape[1] == Hk, "n_kv_heads mismatch between k/v")
     _check(Hk > 0 and H % Hk == 0, "n_heads must be divisible by n_kv_heads (GQA)")
     _check(d in (64, 128), "Only head_dim=64 or head_dim=128 is supported")
     _check(mask.shape[1] == 1 and mask.shape[2] >= Sq and mask.shape[3] >= Sk,
            "mask shape must be (B, 1, >=Sq, k-dim >= Sk)")
+    # Not in the reference, which trusts both (the C ABI carries one Hk and
+    # addresses every tensor on q's device): checked after the reference's own.
+    _check(k.device == q.device and v.device == q.device and mask.device == q.device,
+           "q, k, v and mask must be on the same device")
+    _check(v.shape[1] == Hk, "n_kv_heads mismatch between k/v")
 
 
-def make_params(q, k, v, mask, out, num_splits: int = 0) -> _lib.Params:
-    """Fill the C-ABI params (strides in elements) from validated tensors."""
+def make_params(q, k, v, mask, out, num_splits: int = 0, variant=None) -> _lib.Params:
+    """Fill the C-ABI params (strides in elements) from validated tensors.
+    ``variant`` (a ``_lib.Variant``) is referenced, not copied: keep it alive
+    while the params are in use."""
     qs, ks, vs, os_, ms = q.stride(), k.stride(), v.stride(), out.stride(), mask.stride()
     B, H, Sq, d = q.shape
-    return _lib.Params(
+    p = _lib.Params(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), mask.data_ptr(), out.data_ptr(),
         qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
         os_[0], os_[1], os_[2], ms[0], ms[2],
         B, H, k.shape[1], Sq, k.shape[2], mask.shape[2], mask.shape[3], d,
         _lib.BF16 if q.dtype == torch.bfloat16 else _lib.FP16,
         1.0 / math.sqrt(d), num_splits)
+    if variant is not None:
+        p.variant = ctypes.pointer(variant)
+    return p
 
 
 def mha_fwd_with_mask_hip(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                          mask: torch.Tensor, num_splits: int = 0) -> torch.Tensor:
+                          mask: torch.Tensor, num_splits: int = 0, variant=None) -> torch.Tensor:
     """The device implementation (dispatch key CUDA = HIP on PyTorch-ROCm).
 
     ``num_splits`` = 0 lets the library plan the split; a positive value
-    forces that many KV splits (tests use it to pin split invariance)."""
+    forces that many KV splits (tests use it to pin split invariance).
+    ``variant`` (a ``_lib.Variant``, default None = the library's plan) forces
+    kernel variants for parity tests and tuning."""
     validate(q, k, v, mask)
     out = torch.empty_like(q)
     if out.numel() == 0:
         return out
-    p = make_params(q, k, v, mask, out, num_splits)
+    p = make_params(q, k, v, mask, out, num_splits, variant)
     dev = q.get_device()
     if dev == torch.cuda.current_device():
         ws = _launch(p, q.device, dev)
@@ -173,14 +184,9 @@ def register() -> None:
     _registered = True
 
 
-def num_splits_for(q, k, v, mask) -> int:
+def num_splits_for(q, k, v, mask, variant=None) -> int:
     """The split count the library would use for these inputs (host query)."""
     validate(q, k, v, mask)
-    p = make_params(q, k, v, mask, q)   # planning reads shapes only; q stands in for out
+    p = make_params(q, k, v, mask, q, 0, variant)   # planning reads shapes only; q stands in for out
     with torch.cuda.device(q.device):
         return _lib.num_splits(p)
-
-
-def env_num_splits() -> int | None:
-    val = os.environ.get("MI355_FA_NUM_SPLITS")
-    return int(val) if val and val.isdigit() and int(val) > 0 else None

@@ -306,7 +306,9 @@ class FAOps:
     # offline build
     def _provenance(self, targets: list, extra: list) -> dict:
         h = hashlib.sha256()
-        for src in [Path(_build.SRC), *sorted(Path(_build.INCLUDE).glob("*.h"))]:
+        csrc = Path(_build.SRC).parent
+        for src in [Path(_build.SRC), *sorted(csrc.glob("*.h")), *sorted(csrc.glob("*.inc")),
+                    *sorted(Path(_build.INCLUDE).glob("*.h"))]:
             h.update(src.name.encode() + b"\0" + src.read_bytes())
         flags = [f for f in _build.HIPCC_FLAGS if not f.startswith("--offload-arch=")] + extra
         try:

@@ -2,7 +2,6 @@
 
     python -m custom_ops_amd.prof_collect --config cfg2 --out prof_out
     python -m custom_ops_amd.prof_collect --config cfg2 --stall --out prof_out
-    python -m custom_ops_amd.prof_collect --hbm --out prof_out
     python -m custom_ops_amd.prof_collect --bench --out prof_out
 
 Runs, each as its own rocprofv3 process under a hard time limit (this process
@@ -61,7 +60,6 @@ STALL_PASSES = {
                "SQ_LDS_UNALIGNED_STALL", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES",
                "GRBM_GUI_ACTIVE"],
 }
-HBM_MIB = 2048
 
 
 def workload_cmd(cfg: str, iters: int, bcast: bool = False) -> list[str]:
@@ -73,10 +71,6 @@ def rocprof_cmd(name: str, outdir: str, cfg: str, iters: int) -> list[str]:
     if name == "bench":
         return ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", outdir, "--",
                 sys.executable, os.path.join(ROOT, "bench.py"), "--no-cpu", "--no-configs"]
-    if name == "hbm":
-        return ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv", "-d", outdir, "--",
-                sys.executable, "-m", "custom_ops_amd.prof_workload", "--hbm-read-mib", str(HBM_MIB),
-                "--iters", str(iters)]
     args = PASSES.get(name) or STALL_PASSES[name]
     return ["rocprofv3", *args, "--output-format", "csv", "-d", outdir, "--",
             *workload_cmd(cfg, iters, bcast=name.endswith("_bcast"))]
@@ -140,36 +134,6 @@ def write_summary(path: str, title: str, cmds: list[str], body: list[str]) -> No
     print(txt, flush=True)
 
 
-def hbm_main(args) -> None:
-    """Cold HBM read ceiling: the probe kernel reading 2 GiB after a 512 MiB
-    flush, per pass; GB/s = bytes / the kernel's average duration."""
-    d = run_pass("hbm", args.out, "", args.iters)
-    stats = rows(d, "kernel_stats.csv")
-    probe = [r for r in stats if "hbm_read_kernel" in r["Name"]]
-    if not probe:
-        raise RuntimeError("no hbm_read_kernel dispatch in the kernel trace")
-    avg_ns = float(probe[0]["AverageNs"])
-    nbytes = HBM_MIB * 1024 * 1024
-    body = ["kernel trace (--stats):",
-            f"  {'name':<60} {'calls':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9}"]
-    for r in stats:
-        body.append(f"  {r['Name'][:60]:<60} {int(r['Calls']):>6} {float(r['AverageNs'])/1e3:>9.2f} "
-                    f"{float(r['MinNs'])/1e3:>9.2f} {float(r['MaxNs'])/1e3:>9.2f}")
-    body += ["", "derived:",
-             f"  bytes_read_per_pass                {nbytes}",
-             f"  avg_duration_us                    {avg_ns / 1e3:.6g}",
-             f"  min_duration_us                    {float(probe[0]['MinNs']) / 1e3:.6g}",
-             f"  read_gbps_avg                      {nbytes / (avg_ns * 1e-9) / 1e9:.6g}",
-             f"  read_gbps_best                     {nbytes / (float(probe[0]['MinNs']) * 1e-9) / 1e9:.6g}",
-             f"  fraction_of_8TBps                  {nbytes / (avg_ns * 1e-9) / 8e12:.4g}"]
-    write_summary(os.path.join(args.out, "hbm_read_ceiling.txt"),
-                  "# rocprofv3 summary: cold HBM read ceiling (hbm_read_kernel, 2 GiB per pass, "
-                  "512 MiB flush before each)",
-                  [f"python -m custom_ops_amd.prof_collect --hbm --iters {args.iters}",
-                   "cd /tmp && TMPDIR=/tmp PYTHONPATH=<repo> " + " ".join(rocprof_cmd("hbm", "<out>/raw/hbm", "", args.iters))],
-                  body)
-
-
 def bench_main(args) -> None:
     """Kernel trace of bench.py's own timed run (cfg2): the attention kernel's
     average over every launch, and over the cold steps alone (the launches
@@ -226,8 +190,7 @@ def stall_main(args, cfg) -> None:
 
 
 POWER_LOADS = [("cfg2", ["--config", "cfg2"]), ("cfg3", ["--config", "cfg3"]), ("cfg4", ["--config", "cfg4"]),
-               ("cfg5", ["--config", "cfg5"]), ("mfma_random", ["--mfma", "random"]),
-               ("mfma_const", ["--mfma", "const"])]
+               ("cfg5", ["--config", "cfg5"])]
 
 
 def smi_sample() -> tuple[float | None, list[float]]:
@@ -257,8 +220,7 @@ def smi_sample() -> tuple[float | None, list[float]]:
 def power_main(args) -> None:
     """Steady-state socket power and XCD clocks: each workload runs back to
     back for --loop-s seconds in its own process; amd-smi is sampled twice in
-    the second half. The MFMA probe with random and with constant operands
-    gives the matrix core's sustained rate at the power and clock it can hold."""
+    the second half."""
     from custom_ops_amd.workloads import CONFIGS
     env = dict(os.environ, PYTHONPATH=ROOT)
     idle_w, idle_c = smi_sample()
@@ -280,21 +242,14 @@ def power_main(args) -> None:
         last = [l for l in out.splitlines() if l.startswith("prof_workload")][-1]
         watts = [w for w, _ in samples if w is not None]
         clocks = [c for _, cs in samples for c in cs[:8]]
-        if name.startswith("cfg"):
-            us = float(last.split(",")[-1].split()[0])
-            tflops = CONFIGS[name].flops / (us * 1e-6) / 1e12
-            rate = f"{us:.1f} us = {tflops:.0f} TFLOP/s"
-        else:
-            tflops = float(last.split(",")[-1].split()[0])
-            rate = f"{tflops:.0f} TFLOP/s"
+        us = float(last.split(",")[-1].split()[0])
+        tflops = CONFIGS[name].flops / (us * 1e-6) / 1e12
+        rate = f"{us:.1f} us = {tflops:.0f} TFLOP/s"
         rates[name] = tflops
         w = max(watts) if watts else float("nan")
         cl = (f"{min(clocks):.0f}/{sum(clocks) / len(clocks):.0f}/{max(clocks):.0f}" if clocks else "n/a")
         body.append(f"  {name:<12} {rate:>22} {w:>9.0f} {cl:>30}")
-    body += ["", "derived:",
-             f"  cfg2 / mfma_random                 {rates['cfg2'] / rates['mfma_random']:.3f}",
-             f"  mfma_random / 2500 TFLOP/s         {rates['mfma_random'] / 2500:.3f}",
-             f"  mfma_const / 2500 TFLOP/s          {rates['mfma_const'] / 2500:.3f}"]
+    body += ["", "derived:"] + [f"  {n} / 2500 TFLOP/s{'':<17} {r / 2500:.3f}" for n, r in rates.items()]
     write_summary(os.path.join(args.out, "power_clocks.txt"),
                   "# socket power and XCD clocks under each workload (amd-smi, steady state)",
                   [f"python -m custom_ops_amd.prof_collect --power --loop-s {args.loop_s}"]
@@ -309,7 +264,6 @@ def main() -> None:
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--out", default=os.path.join(ROOT, "prof_out"))
-    ap.add_argument("--hbm", action="store_true", help="cold HBM read ceiling instead")
     ap.add_argument("--stall", action="store_true", help="wave-state counters instead")
     ap.add_argument("--bench", action="store_true", help="kernel trace of bench.py's timed run instead")
     ap.add_argument("--power", action="store_true", help="socket power and clocks per workload instead")
@@ -319,9 +273,6 @@ def main() -> None:
     os.makedirs(args.out, exist_ok=True)
     sys.path.insert(0, ROOT)
     from custom_ops_amd.workloads import CONFIGS
-    if args.hbm:
-        hbm_main(args)
-        return
     if args.bench:
         bench_main(args)
         return

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MI355_FA_ABI_VERSION 1
+#define MI355_FA_ABI_VERSION 2
 
 /* Error codes returned by the entry points (0 = success). */
 enum {
@@ -42,6 +42,25 @@ enum {
 
 /* Element type of q/k/v/mask/out (all five share it). */
 enum { MI355_FA_FP16 = 0, MI355_FA_BF16 = 1 };
+
+/*
+ * Kernel-variant selection, for parity tests and tuning only. Every field 0
+ * (or mi355_fa_params.variant NULL) leaves each choice to the library's plan;
+ * a nonzero field forces one choice for this call and nothing else. No
+ * counterpart in the reference, whose kernel variants are compile-time
+ * template choices (csrc/fa/fa_fwd_launch.h:262-309).
+ */
+typedef struct mi355_fa_variant {
+  int32_t waves;     /* 0 | 4 | 8: waves per workgroup (128 or 256 query rows)         */
+  int32_t pack;      /* 0 | 1 | 2 | 4: GQA q-heads per workgroup (capped by H/Hk)      */
+  int32_t order;     /* 0 | 1 heads fastest | 2 m-blocks fastest (workgroup order)     */
+  int32_t loop;      /* 0 | 1 32-row asm loop | 2 64-row asm loop | 3 ping-pong loop
+                        (fp16: the 32-row loop) | -1 compiled kernel only             */
+  int32_t fuse;      /* 0 | -1: two-split launches keep the combine kernel             */
+  int32_t live;      /* 0 | 1 on everywhere | -1 off: live-range narrowing             */
+  int32_t deep;      /* 0 | -1: 4-wave grids keep two K/V stages                       */
+  int32_t mask_mfma; /* 0 | -1: the compiled kernel widens bf16 masks on the VALU      */
+} mi355_fa_variant;
 
 /*
  * Launch parameters. Strides are in ELEMENTS. Layouts:
@@ -81,6 +100,8 @@ typedef struct mi355_fa_params {
    * words (may be NULL when no split is planned; its contents need no clearing). */
   void* workspace;
   size_t workspace_bytes;
+  /* Test/tuning variant selection (NULL = the library's plan); see above. */
+  const mi355_fa_variant* variant;
 } mi355_fa_params;
 
 /* Run the forward pass on `stream` (a hipStream_t; NULL = legacy default stream).
@@ -102,7 +123,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
 int mi355_fa_fwd_noalloc(const mi355_fa_params* p, void* stream, char* err, size_t errlen);
 
 /* Number of KV splits the launcher will use for these params (after its plan,
- * the MI355_FA_NUM_SPLITS override and clamping). */
+ * the MI355_FA_NUM_SPLITS override, read once per process, and clamping). */
 int mi355_fa_num_splits(const mi355_fa_params* p);
 
 /* Bytes of workspace mi355_fa_fwd needs for these params (0 when unsplit). */

@@ -68,11 +68,11 @@ def make_case(b, h, hk, sq, sk, d, kind, dtype, seed=42, extra_rows=0, extra_col
     return q, k, v, m.contiguous().to(dtype)
 
 
-def run(ops, case, dev, name, num_splits=0):
+def run(ops, case, dev, name, num_splits=0, waves=0):
     q, k, v, m = (t.to(dev) for t in case)
-    if num_splits:
-        from custom_ops_amd import mha_fwd_with_mask
-        out = mha_fwd_with_mask(q, k, v, m, num_splits=num_splits)
+    if num_splits or waves:
+        from custom_ops_amd import Variant, mha_fwd_with_mask
+        out = mha_fwd_with_mask(q, k, v, m, num_splits=num_splits, variant=Variant(waves=waves))
     else:
         out = ops.mha_fwd_with_mask(q, k, v, m)
     torch.cuda.synchronize()
@@ -181,19 +181,18 @@ def test_split_invariance(ops, gpu, splits):
     assert torch.all(out[:, :, 5, :] == 0)
 
 
-@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp16"])
 @pytest.mark.parametrize("sk,extra_cols", [(1000, 0), (777, 3)])
-def test_workgroup_variants(ops, gpu, monkeypatch, waves, splits, d, dtype, sk, extra_cols):
+def test_workgroup_variants(ops, gpu, waves, splits, d, dtype, sk, extra_cols):
     """Both workgroup sizes (4 waves / BM 128, 8 waves / BM 256), forced through
     the single-pass and split-KV epilogues, with 16-byte-aligned mask rows (LDS
     DMA) and unaligned ones (register path)."""
-    monkeypatch.setenv("MI355_FA_WAVES", waves)
     case = make_case(2, 4, 2, 300, sk, d, "inf_random", dtype, extra_cols=extra_cols)
     case[3][1, :, 17, :] = float("-inf")
-    out, _ = run(ops, case, gpu, f"w{waves} s{splits} d{d} sk{sk}", num_splits=splits)
+    out, _ = run(ops, case, gpu, f"w{waves} s{splits} d{d} sk{sk}", num_splits=splits, waves=waves)
     assert torch.all(out[1, :, 17, :] == 0)
 
 
@@ -218,23 +217,22 @@ def _skip_mask(kind, b, sq, sk, g):
 
 
 @pytest.mark.parametrize("kind", ["causal", "window", "dead_stripes", "pad_rows_cols"])
-@pytest.mark.parametrize("waves", ["4", "8"])
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float16, 64)],
                          ids=["bf16d128", "fp16d64"])
-def test_dead_mask_blocks(ops, gpu, monkeypatch, kind, waves, splits, dtype, d):
+def test_dead_mask_blocks(ops, gpu, kind, waves, splits, dtype, d):
     """Masks with whole 32-row x 64-key blocks at -inf (a wave skips the
     softmax / PV work of a tile in which none of its rows sees a key): results
     match the fp32 reference, and rows that see no key are exactly 0."""
-    from custom_ops_amd import mha_fwd_with_mask
-    monkeypatch.setenv("MI355_FA_WAVES", waves)
+    from custom_ops_amd import Variant, mha_fwd_with_mask
     g = torch.Generator().manual_seed(7)
     b, h, hk, sq, sk = 2, 4, 2, 700, 1500
     q = _rand((b, h, sq, d), g).to(dtype).to(gpu)
     k = _rand((b, hk, sk, d), g).to(dtype).to(gpu)
     v = _rand((b, hk, sk, d), g).to(dtype).to(gpu)
     m = _skip_mask(kind, b, sq, sk, g).to(dtype).to(gpu)
-    out = mha_fwd_with_mask(q, k, v, m, num_splits=splits)
+    out = mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=Variant(waves=waves))
     torch.cuda.synchronize()
     assert_close(out, ref_attn_torch(q, k, v, m), f"dead blocks {kind} w{waves} s{splits} d{d}")
     dead_rows = torch.isinf(m).all(-1).squeeze(1)          # [b, sq]
@@ -296,19 +294,17 @@ def _sweep_cases_large(n=24, seed=77):
             continue
         cases.append((len(cases), b, h, hk, sq, sk, d, rnd.choice(["bf16", "fp16"]),
                       rnd.choice(kinds), rnd.choice([(0, 0), (0, 0), (5, 3)]),
-                      rnd.choice([0, 0, 0, 3]), rnd.choice(["", "", "4", "8"])))
+                      rnd.choice([0, 0, 0, 3]), rnd.choice([0, 0, 4, 8])))
     return cases
 
 
 @pytest.mark.parametrize("case", _sweep_cases_large(), ids=lambda c: f"large{c[0]}")
-def test_random_shape_sweep_large(ops, gpu, monkeypatch, case):
+def test_random_shape_sweep_large(ops, gpu, case):
     i, b, h, hk, sq, sk, d, dtype, kind, (pad_r, pad_c), splits, waves = case
-    if waves:
-        monkeypatch.setenv("MI355_FA_WAVES", waves)
     dt = torch.bfloat16 if dtype == "bf16" else torch.float16
     c = make_case(b, h, hk, sq, sk, d, kind, dt, seed=5000 + i, extra_rows=pad_r,
                   extra_cols=pad_c)
-    out, _ = run(ops, c, gpu, f"large{i} {case[1:]}", num_splits=splits)
+    out, _ = run(ops, c, gpu, f"large{i} {case[1:]}", num_splits=splits, waves=waves)
     rows_dead = torch.isinf(c[3][:, 0, :sq, :sk].float()).all(-1)
     assert torch.all(out.permute(0, 2, 1, 3)[rows_dead.to(gpu)] == 0)
 

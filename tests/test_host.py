@@ -30,26 +30,31 @@ def test_header_symbols_exported(lib):
     assert set(names) == set(_lib.EXPORTED)
     for n in names:
         assert hasattr(lib, n), f"{n} not exported"
-    assert lib.mi355_fa_abi_version() == 1
+    assert lib.mi355_fa_abi_version() == _lib.ABI_VERSION == 2
     assert b"gfx950" in lib.mi355_fa_build_info()
 
 
-def test_params_struct_layout_matches_header():
-    """ctypes mirror has the header's field order; size is a multiple of 8."""
-    from custom_ops_amd import _lib
-    src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
-    body = src[src.index("typedef struct mi355_fa_params"):src.index("} mi355_fa_params;")]
+def _struct_fields(src, name):
+    body = src[src.index(f"typedef struct {name}"):src.index(f"}} {name};")]
     fields = []
     for line in body.splitlines()[1:]:
         line = line.strip().rstrip(";")
         if not line:
             continue
-        decl = line.split(None, 1)[1] if not line.startswith("const void") else line[len(
-            "const void* "):]
-        for part in decl.split(","):
-            fields.append(part.strip().lstrip("*").strip())
-    assert [f[0] for f in _lib.Params._fields_] == fields
+        # "<type> a, b, c" or "<type>* a": the names are the last word of each part
+        fields += [re.findall(r"\w+", part)[-1] for part in line.split(",")]
+    return fields
+
+
+def test_params_struct_layout_matches_header():
+    """ctypes mirrors have the header's field order; sizes are multiples of 8 / 4."""
+    from custom_ops_amd import _lib
+    src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    assert [f[0] for f in _lib.Params._fields_] == _struct_fields(src, "mi355_fa_params")
+    assert [f[0] for f in _lib.Variant._fields_] == _struct_fields(src, "mi355_fa_variant")
     assert ctypes.sizeof(_lib.Params) % 8 == 0
+    assert ctypes.sizeof(_lib.Variant) == 4 * len(_lib.Variant._fields_)
+    assert _lib.Params.variant.offset == ctypes.sizeof(_lib.Params) - 8
 
 
 def _params(**kw):
@@ -224,6 +229,7 @@ def test_validation_messages_on_host():
         ((q, k, Fake((1, 2, 8, 64), contig=False), m), "v must be contiguous"),
         ((q, k, k, Fake((1, 1, 8, 8, 1))), "mask must be 4D"),
         ((q, Fake((1, 0, 8, 64)), Fake((1, 0, 8, 64)), m), "divisible"),
+        ((q, k, Fake((1, 4, 8, 64)), m), "n_kv_heads mismatch between k/v"),
     ]
     assert fa._valid(q, k, k, m)
     for args, msg in cases:

@@ -155,8 +155,7 @@ def test_generated_loop_is_current():
     import os
     import sys
     gen = os.path.join(os.path.dirname(build.SRC), "gen_fa_loop.py")
-    env = {k: v for k, v in os.environ.items() if k != "W64_ABLATE"}
-    res = subprocess.run([sys.executable, gen, "--check"], env=env, timeout=300)
+    res = subprocess.run([sys.executable, gen, "--check"], timeout=300)
     assert res.returncode == 0, "fa_loop.inc differs from gen_fa_loop.py's output"
 
 
@@ -232,3 +231,79 @@ def test_missed_occupancy_target_is_reported():
     assert len(missed_occupancy(err)) == 1
     assert missed_occupancy("warning: inline asm clobber list contains reserved registers: M0\n") == []
 
+
+
+def _functions(isa):
+    """(name, lines) of every kernel body in the assembly."""
+    import re
+    out, name, body = [], None, []
+    for line in isa.splitlines():
+        m = re.match(r"^(_Z\w+):", line)
+        if m:
+            name, body = m.group(1), []
+            continue
+        if name is None:
+            continue
+        body.append(line.strip())
+        if line.strip().startswith("s_endpgm"):
+            out.append((name, body))
+            name = None
+    return out
+
+
+def _fused_tail_ordering(body):
+    """Problems with the fused split tail's ordering in one kernel body (empty
+    when it is right, or when the kernel has no ticket atomic)."""
+    code = [l for l in body if l and not l.startswith(";") and not l.startswith(".")]
+    cas = [i for i, l in enumerate(code) if "atomic_cmpswap" in l]
+    bad = []
+    for i in cas:
+        bar = max((j for j in range(i) if code[j].startswith("s_barrier")), default=None)
+        if bar is None:
+            bad.append("no s_barrier before the ticket CAS")
+            continue
+        wait = max((j for j in range(bar) if code[j].startswith("s_waitcnt") and "vmcnt(0)" in code[j]),
+                   default=None)
+        if wait is None:
+            bad.append("no s_waitcnt vmcnt(0) before the barrier that precedes the CAS")
+            continue
+        if any(code[j].startswith(("buffer_store", "global_store", "flat_store")) for j in range(wait, i)):
+            bad.append("a store between the vmcnt(0) wait and the CAS")
+        last = max((j for j in range(wait) if code[j].startswith("buffer_store")), default=None)
+        if last is None or "sc1" not in code[last]:
+            bad.append("the last partial store before the wait is not sc1")
+        for l in code[i + 1:]:
+            if l.startswith("buffer_load") and "sc1" not in l:
+                bad.append(f"buffer load after the CAS without sc1: {l}")
+    return bad
+
+
+def test_fused_tail_ordering_in_the_assembly(isa):
+    """The fused split tail's release and acquire are built from instruction
+    order and cache-policy bits (see ticket_arrive in csrc/fa_fwd.hip): every
+    kernel with a ticket CAS must show, in its assembly, an s_waitcnt vmcnt(0)
+    and an s_barrier between its last (sc1) partial store and the CAS, no store
+    in between, and sc1 on every buffer load after the CAS."""
+    checked = 0
+    for name, body in _functions(isa):
+        if not any("atomic_cmpswap" in l for l in body):
+            continue
+        checked += 1
+        assert not _fused_tail_ordering(body), (name, _fused_tail_ordering(body))
+    assert checked >= 4, checked
+
+
+@pytest.mark.parametrize("body,ok", [
+    (["buffer_store_dwordx4 v[1:4], v0, s[4:7], 0 offen sc1", "s_waitcnt vmcnt(0)", "s_barrier",
+      "flat_atomic_cmpswap_x2 v[2:3], v[4:5], v[6:9] sc0", "buffer_load_dwordx4 v[1:4], v0, s[4:7], 0 offen sc1",
+      "s_endpgm"], True),
+    (["buffer_store_dwordx4 v[1:4], v0, s[4:7], 0 offen sc1", "s_barrier",
+      "flat_atomic_cmpswap_x2 v[2:3], v[4:5], v[6:9] sc0", "s_endpgm"], False),
+    (["buffer_store_dwordx4 v[1:4], v0, s[4:7], 0 offen", "s_waitcnt vmcnt(0)", "s_barrier",
+      "flat_atomic_cmpswap_x2 v[2:3], v[4:5], v[6:9] sc0", "s_endpgm"], False),
+    (["buffer_store_dwordx4 v[1:4], v0, s[4:7], 0 offen sc1", "s_waitcnt vmcnt(0)", "s_barrier",
+      "flat_atomic_cmpswap_x2 v[2:3], v[4:5], v[6:9] sc0", "buffer_load_dwordx4 v[1:4], v0, s[4:7], 0 offen",
+      "s_endpgm"], False),
+])
+def test_fused_tail_ordering_check_catches_violations(body, ok):
+    assert (not _fused_tail_ordering(body)) == ok

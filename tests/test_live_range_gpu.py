@@ -1,8 +1,7 @@
 """Live-range narrowing (each workgroup runs only the KV tiles from the first to
 the last one in which its rows' mask has a visible entry, and the splits share
 that range): parity on masks with dead edges, for every tile-loop form, with
-narrowing forced on (MI355_FA_LIVE=1) and off (=0), each in a fresh process
-(the mode and the form are read once per process).
+narrowing forced on (``Variant(live=1)``) and off (``live=-1``).
 
   * every output against the fp32 torch restatement of the reference op
     (tests/test_mha_fwd_with_mask.py:38-53 of the reference) at the suite's
@@ -17,109 +16,88 @@ mask rows past Sq that are visible (ignored), visible trap columns past Sk
 (ignored), unaligned mask rows (Sk % 8 != 0), GQA packing, fp16, d = 64, and
 forced split counts.
 """
-import json
-import os
-import subprocess
-import sys
-import textwrap
-
 import pytest
+import torch
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+from tests._ref import assert_close, ref_attn_torch
 
-CODE = textwrap.dedent("""
-    import hashlib, json, torch
-    from custom_ops_amd import ops, mha_fwd_with_mask
-    from tests._ref import ref_attn_torch, assert_close
-    ops.ensure_loaded()
-    NEG = float("-inf")
+NEG = float("-inf")
 
-    def mask_of(kind, b, sq, sk, skm, msq, g):
-        i = torch.arange(msq).view(msq, 1)
-        j = torch.arange(skm).view(1, skm)
-        m = torch.zeros(b, 1, msq, skm)
-        if kind == "causal":
-            m.masked_fill_((j > i).expand(b, 1, msq, skm), NEG)
-        elif kind == "window":
-            off = sk - sq
-            vis = (j <= i + off) & (j > i + off - 300)
-            m.masked_fill_((~vis).expand(b, 1, msq, skm), NEG)
-        elif kind == "pad":
-            m[..., :500] = NEG
-            m[..., sk - 1000:] = NEG
-        elif kind == "dead_block":
-            m[:, :, :300, :] = NEG
-        elif kind == "last_tile":
-            m[..., : sk - 5] = NEG
-        elif kind == "first_key":
-            m[..., 1:] = NEG
-        elif kind == "rows_past_sq":
-            m[:, :, :sq, :] = NEG
-            m[:, :, :sq, sk // 2: sk // 2 + 70] = 0.0
-        elif kind == "trap_cols":
-            m[..., : sk - 100] = NEG
-        else:
-            raise ValueError(kind)
-        m.masked_fill_(torch.rand(b, 1, msq, skm, generator=g) < 0.05, NEG)
-        if kind == "trap_cols":
-            m[..., sk:] = 0.0          # visible, but past Sk: ignored
-        if kind == "rows_past_sq":
-            m[:, :, sq:, :] = 0.0      # visible, but rows past Sq: ignored
-        return m
 
-    cases = [  # kind, b, h, hk, sq, sk, d, dtype, splits (0: the plan's), extra mask cols, extra mask rows
-        ("causal", 1, 4, 4, 1000, 1000, 128, torch.bfloat16, 0, 0, 0),
-        ("causal", 1, 4, 4, 600, 1000, 128, torch.bfloat16, 1, 0, 0),
-        ("window", 2, 8, 2, 700, 2500, 128, torch.bfloat16, 1, 0, 0),
-        ("window", 2, 8, 2, 700, 2500, 128, torch.bfloat16, 3, 0, 0),
-        ("window", 1, 16, 4, 1000, 4099, 128, torch.bfloat16, 0, 0, 0),
-        ("pad", 1, 4, 1, 300, 3000, 128, torch.bfloat16, 1, 0, 0),
-        ("pad", 1, 4, 1, 300, 3000, 128, torch.bfloat16, 7, 0, 0),
-        ("dead_block", 1, 2, 2, 600, 900, 128, torch.bfloat16, 1, 0, 0),
-        ("dead_block", 1, 2, 2, 600, 900, 128, torch.bfloat16, 2, 0, 0),
-        ("last_tile", 1, 2, 1, 256, 1029, 128, torch.bfloat16, 1, 0, 0),
-        ("last_tile", 1, 2, 1, 256, 1029, 128, torch.bfloat16, 4, 0, 0),
-        ("first_key", 1, 2, 2, 256, 2048, 128, torch.bfloat16, 1, 0, 0),
-        ("rows_past_sq", 1, 2, 2, 200, 1024, 128, torch.bfloat16, 1, 0, 56),
-        ("trap_cols", 1, 2, 2, 256, 1030, 128, torch.bfloat16, 1, 10, 0),
-        ("window", 1, 4, 4, 512, 2048, 128, torch.float16, 1, 0, 0),
-        ("window", 1, 4, 4, 512, 2048, 64, torch.bfloat16, 1, 0, 0),
-        ("causal", 1, 4, 2, 512, 512, 64, torch.float16, 2, 0, 0),
-    ]
-    res = []
-    for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr) in enumerate(cases):
+def mask_of(kind, b, sq, sk, skm, msq, g):
+    i = torch.arange(msq).view(msq, 1)
+    j = torch.arange(skm).view(1, skm)
+    m = torch.zeros(b, 1, msq, skm)
+    if kind == "causal":
+        m.masked_fill_((j > i).expand(b, 1, msq, skm), NEG)
+    elif kind == "window":
+        off = sk - sq
+        vis = (j <= i + off) & (j > i + off - 300)
+        m.masked_fill_((~vis).expand(b, 1, msq, skm), NEG)
+    elif kind == "pad":
+        m[..., :500] = NEG
+        m[..., sk - 1000:] = NEG
+    elif kind == "dead_block":
+        m[:, :, :300, :] = NEG
+    elif kind == "last_tile":
+        m[..., : sk - 5] = NEG
+    elif kind == "first_key":
+        m[..., 1:] = NEG
+    elif kind == "rows_past_sq":
+        m[:, :, :sq, :] = NEG
+        m[:, :, :sq, sk // 2: sk // 2 + 70] = 0.0
+    elif kind == "trap_cols":
+        m[..., : sk - 100] = NEG
+    else:
+        raise ValueError(kind)
+    m.masked_fill_(torch.rand(b, 1, msq, skm, generator=g) < 0.05, NEG)
+    if kind == "trap_cols":
+        m[..., sk:] = 0.0          # visible, but past Sk: ignored
+    if kind == "rows_past_sq":
+        m[:, :, sq:, :] = 0.0      # visible, but rows past Sq: ignored
+    return m
+
+
+CASES = [  # kind, b, h, hk, sq, sk, d, dtype, splits (0: the plan's), extra mask cols, extra mask rows
+    ("causal", 1, 4, 4, 1000, 1000, 128, torch.bfloat16, 0, 0, 0),
+    ("causal", 1, 4, 4, 600, 1000, 128, torch.bfloat16, 1, 0, 0),
+    ("window", 2, 8, 2, 700, 2500, 128, torch.bfloat16, 1, 0, 0),
+    ("window", 2, 8, 2, 700, 2500, 128, torch.bfloat16, 3, 0, 0),
+    ("window", 1, 16, 4, 1000, 4099, 128, torch.bfloat16, 0, 0, 0),
+    ("pad", 1, 4, 1, 300, 3000, 128, torch.bfloat16, 1, 0, 0),
+    ("pad", 1, 4, 1, 300, 3000, 128, torch.bfloat16, 7, 0, 0),
+    ("dead_block", 1, 2, 2, 600, 900, 128, torch.bfloat16, 1, 0, 0),
+    ("dead_block", 1, 2, 2, 600, 900, 128, torch.bfloat16, 2, 0, 0),
+    ("last_tile", 1, 2, 1, 256, 1029, 128, torch.bfloat16, 1, 0, 0),
+    ("last_tile", 1, 2, 1, 256, 1029, 128, torch.bfloat16, 4, 0, 0),
+    ("first_key", 1, 2, 2, 256, 2048, 128, torch.bfloat16, 1, 0, 0),
+    ("rows_past_sq", 1, 2, 2, 200, 1024, 128, torch.bfloat16, 1, 0, 56),
+    ("trap_cols", 1, 2, 2, 256, 1030, 128, torch.bfloat16, 1, 10, 0),
+    ("window", 1, 4, 4, 512, 2048, 128, torch.float16, 1, 0, 0),
+    ("window", 1, 4, 4, 512, 2048, 64, torch.bfloat16, 1, 0, 0),
+    ("causal", 1, 4, 2, 512, 512, 64, torch.float16, 2, 0, 0),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("loop", [-1, 1, 2, 3])
+def test_live_range_parity(gpu, loop):
+    from custom_ops_amd import Variant, mha_fwd_with_mask
+    on, off = Variant(loop=loop, live=1), Variant(loop=loop, live=-1)
+    for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr) in enumerate(CASES):
         g = torch.Generator().manual_seed(1000 + n)
         q = (torch.randn(b, h, sq, d, generator=g) * 0.5).to(dt).cuda()
         k = (torch.randn(b, hk, sk, d, generator=g) * 0.5).to(dt).cuda()
         v = (torch.randn(b, hk, sk, d, generator=g) * 0.5).to(dt).cuda()
         m = mask_of(kind, b, sq, sk, sk + xc, sq + xr, g).to(dt).cuda()
-        out = mha_fwd_with_mask(q, k, v, m, num_splits=splits) if splits else ops.mha_fwd_with_mask(q, k, v, m)
-        torch.cuda.synchronize()
         ref = ref_attn_torch(q, k, v, m[:, :, :sq, :sk])
-        assert_close(out, ref, f"case {n} {kind}")
         dead = torch.isinf(m[:, :, :sq, :sk].float()).all(-1)          # [b, 1, sq]
-        assert bool((out.float().masked_select(dead.unsqueeze(-1).expand(b, h, sq, d)) == 0).all())
-        sha = hashlib.sha256(out.view(torch.int16).cpu().numpy().tobytes()).hexdigest()
-        res.append({"case": n, "splits": splits, "sha": sha})
-    print("LIVE-RESULT " + json.dumps(res))
-""")
-
-
-def _run(form, live):
-    env = dict(os.environ, MI355_FA_ASM=form, MI355_FA_LIVE=live, PYTHONPATH=ROOT)
-    res = subprocess.run([sys.executable, "-c", CODE], cwd=ROOT, env=env, capture_output=True,
-                         text=True, timeout=300)
-    assert res.returncode == 0, (res.stdout[-2000:], res.stderr[-3000:])
-    line = [ln for ln in res.stdout.splitlines() if ln.startswith("LIVE-RESULT ")]
-    assert line, res.stdout[-2000:]
-    return json.loads(line[-1][len("LIVE-RESULT "):])
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("form", ["0", "1", "2", "3"])
-def test_live_range_parity(form):
-    on = _run(form, "1")
-    off = _run(form, "0")
-    for a, b in zip(on, off):
-        if a["splits"] == 1:
-            assert a["sha"] == b["sha"], f"form {form} case {a['case']}: narrowed unsplit launch differs"
+        outs = [mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=var) for var in (on, off)]
+        torch.cuda.synchronize()
+        for var, out in zip(("on", "off"), outs):
+            tag = f"loop {loop} live {var} case {n} {kind}"
+            assert_close(out, ref, tag)
+            assert bool((out.float().masked_select(dead.unsqueeze(-1).expand(b, h, sq, d)) == 0).all()), tag
+        if splits == 1:
+            assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), \
+                f"loop {loop} case {n} {kind}: narrowed unsplit launch differs"

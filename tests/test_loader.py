@@ -142,7 +142,7 @@ def test_resealed_mismatches_name_the_section(exported, tmp_path):
             {"recsys_ops::mha_fwd_with_mask": "recsys_ops::mha_fwd_with_mask(Tensor q) -> Tensor"}),
          "contract mismatch (schemas"),
         (lambda md: md["contract"].update({"namespace": "other_ops"}), "contract mismatch (namespace"),
-        (lambda md: md["contract"].update({"abi": 2}), "contract mismatch (abi"),
+        (lambda md: md["contract"].update({"abi": 1}), "contract mismatch (abi"),
         (lambda md: md["runtime"].update({"torch": "1.13"}), "runtime mismatch (torch"),
         (lambda md: md.update({"targets": ["GFX950"]}), "invalid offload target"),
         (lambda md: md["payload"].update({"bytes": 1}), "payload size mismatch"),
