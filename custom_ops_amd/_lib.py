@@ -43,7 +43,7 @@ class Variant(ctypes.Structure):
     see the header for the meaning of each value."""
 
     _fields_ = [(name, ctypes.c_int32) for name in
-                ("waves", "pack", "order", "loop", "fuse", "live", "deep", "mask_mfma")]
+                ("waves", "pack", "order", "loop", "fuse", "live", "deep", "mask_mfma", "stream")]
 
     def __repr__(self) -> str:
         set_ = {n: getattr(self, n) for n, _ in self._fields_ if getattr(self, n)}

@@ -135,15 +135,28 @@ __device__ __forceinline__ i32x4 make_rsrc_words(const void* base, uint32_t byte
 __device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
 }
+// NT: the non-temporal hint, for data each workgroup reads exactly once in a
+// launch (the replacement policy then keeps other lines; cold reads of such a
+// stream run up to 10 % faster).
+template <bool NT = false>
 __device__ __forceinline__ void bload16_lds(i32x4 rs, uint32_t lds_byte, uint32_t voff) {
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_byte);
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
-      :
-      : "s"(m0v), "v"(voff), "s"(rs)
-      : "memory", "m0");
+  if constexpr (NT)
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen nt lds"
+        :
+        : "s"(m0v), "v"(voff), "s"(rs)
+        : "memory", "m0");
+  else
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(m0v), "v"(voff), "s"(rs)
+        : "memory", "m0");
 }
 
 // ── kernel parameters (device copy, passed by value) ──────────────────────────
@@ -173,7 +186,7 @@ struct KParams {
   int n_per_split;   // tiles per split
   int total;         // grid size (workgroups)
   int mask_direct;   // mask rows 16-byte aligned: the mask tile can go by LDS DMA
-  int head_major;    // tile order: heads fastest (else m-blocks fastest)
+  int head_major;    // tile order: 1 heads fastest, 2 heads then splits fastest, 0 m-blocks fastest
   float scale;       // softmax scale (1/sqrt(d) in the reference op)
   // scale·log2(e) and the rescale slack in score units, as float bits: kernel
   // arguments arrive in SGPRs, which the assembly loops take as scalar operands
@@ -189,6 +202,9 @@ struct KParams {
   // bf16, scale < 0.99: the compiled kernel's LDS mask path adds the mask on
   // the matrix core (bf16(1/scale) > 1.0078 makes -max_bf16 overflow to -inf)
   int mask_mfma;
+  // K/V tiles are read by exactly one workgroup each: the compiled kernel
+  // streams them with the non-temporal hint
+  int kv_nt;
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -295,7 +311,12 @@ __device__ __forceinline__ TileIdx tile_index(PT& p) {
   int t = xcd_remap(blockIdx.x, p.total);
   const int ng = p.h / p.pack;   // head groups per batch
   int mb, hg;
-  if (p.head_major) {   // (b, split, m-block, head group): the heads sharing a mask tile run together
+  if (p.head_major == 2) {   // (b, m-block, split, head group): every workgroup reading a row block's mask runs together
+    hg = t % ng;  t /= ng;
+    ti.split = t % p.num_splits;  t /= p.num_splits;
+    mb = t % p.num_m;
+    ti.b = t / p.num_m;
+  } else if (p.head_major) {   // (b, split, m-block, head group): the heads sharing a mask tile run together
     hg = t % ng;  t /= ng;
     mb = t % p.num_m;  t /= p.num_m;
     ti.split = t % p.num_splits;
@@ -442,7 +463,29 @@ __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams
   return pr;
 }
 
-template <bool BF16, int NT, int BMAX, int J, bool REUSE>
+// whether the chunk (8 entries from column cofs of tile tb, cofs in -7 .. 71)
+// holds a visible entry inside its tile and below Sk
+template <bool BF16>
+__device__ __forceinline__ bool live8a(u32x4 v, int cofs, int tb, int sk) {
+  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u;
+  const int lo = -cofs, hi = min(kBN, sk - tb) - cofs;   // entries e with lo <= e < hi count
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    any |= (2 * i >= lo) & (2 * i < hi) & ((v[i] & 0xffffu) != kNeg);
+    any |= (2 * i + 1 >= lo) & (2 * i + 1 < hi) & ((v[i] >> 16) != kNeg);
+  }
+  return any;
+}
+
+// UNALIGNED: the mask rows may start anywhere (2-byte aligned). Every chunk is
+// still read as an aligned 16-byte load: a row whose first entry sits sh
+// bytes past a 16-byte boundary is read from that boundary, 9 chunks per
+// tile, the first and the last holding entries of the neighbouring tiles,
+// which are not counted (an unaligned 16-byte load costs the memory pipeline
+// several aligned ones). Otherwise rows are 16-byte aligned (the launches
+// whose mask goes by LDS DMA) and a tile row is exactly 8 chunks.
+template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool UNALIGNED>
 __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, int rows, const LiveProbe& pr,
                                                uint32_t* red) {
   CKParams& p = kernarg_params(pk);
@@ -460,24 +503,46 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
     return false;
   }
   int lo = lb ? 0 : -1, hi = rb ? nn - 1 : -1;
-  constexpr int kRounds = (8 * BMAX + J * NT - 1) / (J * NT);   // rounds that cover one whole tile
-  const int cpt = nr * 8;                  // 16-byte chunks per tile of these rows
+  constexpr int kCprMax = UNALIGNED ? 9 : 8;                     // chunks per row and tile
+  constexpr int kRounds = (kCprMax * BMAX + J * NT - 1) / (J * NT);   // rounds that cover one whole tile
+  constexpr int NL = kRounds * J;
+  // the batch's mask, from the 16-byte boundary at or below its first entry
+  const uint16_t* mb = p.mask + (int64_t)ti.b * p.m_bs;
+  uint32_t base_mod = 0u;
+  if constexpr (UNALIGNED)
+    base_mod = __builtin_amdgcn_readfirstlane(low_u32(reinterpret_cast<uint64_t>(mb))) & 15u;
+  const rsrc_t rm = make_rsrc_uniform(reinterpret_cast<const uint8_t*>(mb) - base_mod,
+                                      (uint32_t)p.msq * p.m_rs * 2u + base_mod);
+  const int cpr = (UNALIGNED && ((base_mod | (uint32_t)(p.m_rs & 7)) != 0u)) ? 9 : 8;
+  const int cpt = nr * cpr;                // 16-byte chunks per tile of these rows
   int U = (kRounds * J * NT) / cpt;        // tiles per window: 1 .. 32
   U = U > 32 ? 32 : U;
-  const rsrc_t rm = mask_rsrc(p, ti.b);
-  // Each thread's chunks, the same in every step: window slot t, row offset
-  // and column within the tile (one division each, here, not per step)
-  constexpr int NL = kRounds * J;
+  // Each thread's chunks, the same in every step: window slot t, byte offset
+  // of the chunk in tile 0 and (unaligned rows) its first column relative to
+  // its tile (one division each, here, not per step)
   int tj[NL];
   uint32_t roff[NL];
+  int cofs[UNALIGNED ? NL : 1];
 #pragma unroll
   for (int n = 0; n < NL; ++n) {
     const int c = n * NT + tid, t = c / cpt, rem = c - t * cpt;
     tj[n] = t;
-    roff[n] = (uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u;
+    if constexpr (UNALIGNED) {
+      const int r = rem / cpr, k = rem - r * cpr;
+      const uint32_t rowb = base_mod + (uint32_t)(ti.m0 + r) * (uint32_t)p.m_rs * 2u;
+      const uint32_t sh = rowb & 15u;      // the row's first entry, bytes past a boundary
+      roff[n] = rowb - sh + 16u * (uint32_t)k;
+      cofs[n] = 8 * k - (int)(sh >> 1);
+    } else {
+      roff[n] = ((uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u) * 2u;
+    }
   }
-  const int c0 = (tid & 7) * 8;   // NT and cpt are multiples of 8: rem & 7 == tid & 7
+  const int c0 = (tid & 7) * 8;   // aligned rows: NT and cpt are multiples of 8, rem & 7 == tid & 7
   const int sk = p.sk;
+  auto live = [&](u32x4 v, int n, int tile) -> bool {
+    if constexpr (UNALIGNED) return live8a<BF16>(v, cofs[n], tile * kBN, sk);
+    else return live8<BF16>(v, tile * kBN + c0, sk);
+  };
   int L = 0, R = nn - 1;
   for (int step = 0; lo < 0 || hi < 0; ++step) {
     if (L > R) break;                      // every tile scanned and dead
@@ -500,15 +565,15 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
 #pragma unroll
     for (int n = 0; n < NL; ++n) {
       const int t = tj[n];
-      va[n] = bload16(rm, (roff[n] + (uint32_t)(t < ua ? a0 + da * t : L) * kBN) * 2u);
-      vb[n] = bload16(rm, (roff[n] + (uint32_t)(t < ub ? b0 + db * t : L) * kBN) * 2u);
+      va[n] = bload16(rm, roff[n] + (uint32_t)(t < ua ? a0 + da * t : L) * (kBN * 2u));
+      vb[n] = bload16(rm, roff[n] + (uint32_t)(t < ub ? b0 + db * t : L) * (kBN * 2u));
     }
 #pragma unroll
     for (int n = 0; n < NL; ++n) {
       const int t = tj[n];
       const uint32_t bit = 1u << (t & 31);
-      abits |= ((t < ua) & live8<BF16>(va[n], (a0 + da * t) * kBN + c0, sk)) ? bit : 0u;
-      bbits |= ((t < ub) & live8<BF16>(vb[n], (b0 + db * t) * kBN + c0, sk)) ? bit : 0u;
+      abits |= ((t < ua) & live(va[n], n, a0 + da * t)) ? bit : 0u;
+      bbits |= ((t < ub) & live(vb[n], n, b0 + db * t)) ? bit : 0u;
     }
     wg_or2<NT>(abits, bbits, red, step & 1);
     if (both) {
@@ -527,6 +592,9 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   __syncthreads();                         // every wave has read `red` before any DMA lands
   // no visible entry in these rows: an empty range (lo = 0, hi = -1)
   if (lo < 0) { lo = 0; hi = -1; }
+#if MI355_SCAN_TIMING
+  if (lo <= hi) return false;   // timing only: the scan runs, the nominal ranges stand
+#endif
   const int ns = uni(p.num_splits);
   const int per = (hi - lo + 1 + ns - 1) / ns;
   const int nb = min(lo + ti.split * per, hi + 1);
@@ -959,7 +1027,8 @@ struct Attn {
     const i32x4 r = make_rsrc_words(reinterpret_cast<const char*>(kbase) + sh, kbytes - sh);
 #pragma unroll
     for (int i = 0; i < G::kKWaveLoads; ++i)
-      bload16_lds(r, lds_addr(sK) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), k_off[i]);
+      if (p.kv_nt) bload16_lds<true>(r, lds_addr(sK) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), k_off[i]);
+      else bload16_lds<false>(r, lds_addr(sK) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), k_off[i]);
   }
 
   // Mask tile n. MREG: straight into registers, chunk i (8 keys, 16 bytes)
@@ -1021,7 +1090,8 @@ struct Attn {
     const i32x4 r = make_rsrc_words(reinterpret_cast<const char*>(vbase) + sh, vbytes - sh);
 #pragma unroll
     for (int i = 0; i < G::kKWaveLoads; ++i)
-      bload16_lds(r, lds_addr(sV) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), v_off[i]);
+      if (p.kv_nt) bload16_lds<true>(r, lds_addr(sV) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), v_off[i]);
+      else bload16_lds<false>(r, lds_addr(sV) + (uint32_t)((i * G::kWaves + wave) * 64 * 16), v_off[i]);
   }
 
   // u = mask·(1/scale) + K·Qᵀ: the widened, pre-scaled mask tile initialises the
@@ -1280,7 +1350,7 @@ void fa_fwd_kernel(const KParams p) {
   {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
-    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true>(tn, p, G::kBM / p.pack, lp,
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, false>(tn, p, G::kBM / p.pack, lp,
                                                        reinterpret_cast<uint32_t*>(KS(NST - 1)))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
@@ -1420,7 +1490,7 @@ void fa_fwd_kernel_asm(const KParams p) {
     // before the set-up below: its values would be live across the scan, and
     // the registers the scan needs on top of them would spill
     const LiveProbe lp = live_probe<64 * WAVES>(ti, p);
-    narrow_to_live<BF16, 64 * WAVES, 256, 4, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kAsmMBase));
+    narrow_to_live<BF16, 64 * WAVES, 256, 4, false, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kAsmMBase));
   }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1588,7 +1658,7 @@ void fa_fwd_kernel_pp(const KParams p) {
     // before the set-up below: its values would be live across the scan, and
     // the SGPRs the scan needs on top of them would spill
     const LiveProbe lp = live_probe<512>(ti, p);
-    narrow_to_live<true, 512, 256, 4, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kPpMBase));
+    narrow_to_live<true, 512, 256, 4, false, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kPpMBase));
   }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1924,6 +1994,7 @@ struct Plan {
   // 1 = on everywhere, 0 = off.
   int live;
   int mask_mfma_off;   // the compiled kernel widens bf16 masks on the VALU
+  int kv_nt;           // every K/V tile is read by one workgroup: non-temporal loads
 };
 
 // Tile plan: the workgroup size (4 or 8 waves) and split count with the
@@ -1972,6 +2043,7 @@ static int order_head_major(const mi355_fa_params* p, const Plan& pl, int cus,
                             const mi355_fa_variant& v) {
   if (v.order == 1) return 1;
   if (v.order == 2) return 0;
+  if (v.order == 3) return 2;
   const double R = (double)(cus / 8 > 0 ? cus / 8 : 1) * (pl.waves == 4 ? 2 : 1);   // workgroups per XCD round
   const double G = p->h / pl.pack;                                   // head groups (one K/V head each)
   const double M = ceil_div(p->seqlen_q, pl.block_m / pl.pack);      // m-blocks
@@ -1986,7 +2058,12 @@ static int order_head_major(const mi355_fa_params* p, const Plan& pl, int cus,
   // groups fastest, then m-blocks, then splits: ceil(R/G) (split, m-block)
   // mask pieces and min(R, G) groups of each split seen
   const double h_fetch = std::min(up(R, G), M * S) * mk + std::min(R, G) * std::min(S, up(R, G * M)) * kv;
-  return h_fetch < m_fetch ? 1 : 0;
+  // Heads fastest in a split launch: the splits of a row block next, so that
+  // every workgroup reading that block's mask rows (its head groups times its
+  // splits; each one scans them when the mask has dead edges) runs on one XCD
+  // at once (cfg5's shape: 1 % faster on a sliding window and on a dense mask).
+  if (h_fetch < m_fetch) return S > 1 ? 2 : 1;
+  return 0;
 }
 
 static Plan make_plan(const mi355_fa_params* p, int cus) {
@@ -2048,6 +2125,14 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   pl.loop = v.loop < 0 ? 0 : (v.loop >= 1 && v.loop <= 3 ? v.loop : 3);
   pl.live = v.live < 0 ? 0 : (v.live > 0 ? 1 : 2);
   pl.mask_mfma_off = v.mask_mfma < 0 ? 1 : 0;
+  // One m-block per head group and every q-head of a KV head in the same
+  // workgroup: each K/V tile is read by exactly one workgroup of the launch
+  // (split-KV decode shapes such as Sq 128 x Sk 32k), a stream with no reuse
+  // for the caches to keep. Loaded non-temporally, its cold read runs at the
+  // rate a plain streaming read reaches with that hint (7.2 against 6.5 TB/s
+  // on MI355X); a back-to-back repeat of the same call that could have found
+  // part of it in the 256 MiB last-level cache loses that.
+  pl.kv_nt = v.stream < 0 ? 0 : (v.stream > 0 ? 1 : (pl.num_m == 1 && pl.pack == p->h / p->h_k));
   return pl;
 }
 
@@ -2266,6 +2351,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.total = (int)total;
   kp.scale = p->scale_softmax;
   kp.mask_mfma = (p->dtype == MI355_FA_BF16 && p->scale_softmax < 0.99f && !pl.mask_mfma_off) ? 1 : 0;
+  kp.kv_nt = pl.kv_nt;
   {
     const float c2 = p->scale_softmax * kLog2e, slack = kRescaleSlack / p->scale_softmax;
     memcpy(&kp.c2_bits, &c2, 4);

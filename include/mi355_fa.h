@@ -53,13 +53,17 @@ enum { MI355_FA_FP16 = 0, MI355_FA_BF16 = 1 };
 typedef struct mi355_fa_variant {
   int32_t waves;     /* 0 | 4 | 8: waves per workgroup (128 or 256 query rows)         */
   int32_t pack;      /* 0 | 1 | 2 | 4: GQA q-heads per workgroup (capped by H/Hk)      */
-  int32_t order;     /* 0 | 1 heads fastest | 2 m-blocks fastest (workgroup order)     */
+  int32_t order;     /* 0 | 1 heads fastest | 2 m-blocks fastest | 3 heads, then
+                        splits fastest (workgroup order)                           */
   int32_t loop;      /* 0 | 1 32-row asm loop | 2 64-row asm loop | 3 ping-pong loop
                         (fp16: the 32-row loop) | -1 compiled kernel only             */
   int32_t fuse;      /* 0 | -1: two-split launches keep the combine kernel             */
   int32_t live;      /* 0 | 1 on everywhere | -1 off: live-range narrowing             */
   int32_t deep;      /* 0 | -1: 4-wave grids keep two K/V stages                       */
   int32_t mask_mfma; /* 0 | -1: the compiled kernel widens bf16 masks on the VALU      */
+  int32_t stream;    /* 0 | 1 on | -1 off: the compiled kernel loads K/V with the
+                        non-temporal hint (default: when each K/V tile is read by
+                        one workgroup of the launch)                               */
 } mi355_fa_variant;
 
 /*

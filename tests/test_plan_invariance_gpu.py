@@ -1,6 +1,7 @@
 """Plan choices that only move work between workgroups must not change a bit
-of the output: GQA head packing (q-heads per workgroup) and the workgroup
-order (heads or m-blocks fastest) leave every row's arithmetic as it is, once
+of the output: GQA head packing (q-heads per workgroup), the workgroup
+order (heads, heads then splits, or m-blocks fastest) and the non-temporal
+K/V loads leave every row's arithmetic as it is, once
 the workgroup size and the split count are fixed (packing changes the plan's
 cost estimate, and a different split count or kernel legitimately rounds
 differently).
@@ -11,7 +12,8 @@ import torch
 CASES = [(2, 16, 4, 300, 777, torch.bfloat16, 1),
          (1, 8, 1, 513, 1000, torch.float16, 1),
          (2, 8, 2, 128, 4096, torch.bfloat16, 4)]
-SETTINGS = [{}, {"pack": 1}, {"pack": 2}, {"order": 1}, {"order": 2}, {"pack": 1, "order": 2}]
+SETTINGS = [{}, {"pack": 1}, {"pack": 2}, {"order": 1}, {"order": 2}, {"order": 3},
+            {"pack": 1, "order": 2}, {"pack": 2, "order": 3}, {"stream": 1}, {"stream": -1}]
 
 
 @pytest.mark.gpu
