@@ -463,29 +463,7 @@ __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams
   return pr;
 }
 
-// whether the chunk (8 entries from column cofs of tile tb, cofs in -7 .. 71)
-// holds a visible entry inside its tile and below Sk
-template <bool BF16>
-__device__ __forceinline__ bool live8a(u32x4 v, int cofs, int tb, int sk) {
-  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u;
-  const int lo = -cofs, hi = min(kBN, sk - tb) - cofs;   // entries e with lo <= e < hi count
-  bool any = false;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    any |= (2 * i >= lo) & (2 * i < hi) & ((v[i] & 0xffffu) != kNeg);
-    any |= (2 * i + 1 >= lo) & (2 * i + 1 < hi) & ((v[i] >> 16) != kNeg);
-  }
-  return any;
-}
-
-// UNALIGNED: the mask rows may start anywhere (2-byte aligned). Every chunk is
-// still read as an aligned 16-byte load: a row whose first entry sits sh
-// bytes past a 16-byte boundary is read from that boundary, 9 chunks per
-// tile, the first and the last holding entries of the neighbouring tiles,
-// which are not counted (an unaligned 16-byte load costs the memory pipeline
-// several aligned ones). Otherwise rows are 16-byte aligned (the launches
-// whose mask goes by LDS DMA) and a tile row is exactly 8 chunks.
-template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool UNALIGNED>
+template <bool BF16, int NT, int BMAX, int J, bool REUSE>
 __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, int rows, const LiveProbe& pr,
                                                uint32_t* red) {
   CKParams& p = kernarg_params(pk);
@@ -503,46 +481,24 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
     return false;
   }
   int lo = lb ? 0 : -1, hi = rb ? nn - 1 : -1;
-  constexpr int kCprMax = UNALIGNED ? 9 : 8;                     // chunks per row and tile
-  constexpr int kRounds = (kCprMax * BMAX + J * NT - 1) / (J * NT);   // rounds that cover one whole tile
+  constexpr int kRounds = (8 * BMAX + J * NT - 1) / (J * NT);   // rounds that cover one whole tile
   constexpr int NL = kRounds * J;
-  // the batch's mask, from the 16-byte boundary at or below its first entry
-  const uint16_t* mb = p.mask + (int64_t)ti.b * p.m_bs;
-  uint32_t base_mod = 0u;
-  if constexpr (UNALIGNED)
-    base_mod = __builtin_amdgcn_readfirstlane(low_u32(reinterpret_cast<uint64_t>(mb))) & 15u;
-  const rsrc_t rm = make_rsrc_uniform(reinterpret_cast<const uint8_t*>(mb) - base_mod,
-                                      (uint32_t)p.msq * p.m_rs * 2u + base_mod);
-  const int cpr = (UNALIGNED && ((base_mod | (uint32_t)(p.m_rs & 7)) != 0u)) ? 9 : 8;
-  const int cpt = nr * cpr;                // 16-byte chunks per tile of these rows
+  const int cpt = nr * 8;                  // 16-byte chunks per tile of these rows
   int U = (kRounds * J * NT) / cpt;        // tiles per window: 1 .. 32
   U = U > 32 ? 32 : U;
-  // Each thread's chunks, the same in every step: window slot t, byte offset
-  // of the chunk in tile 0 and (unaligned rows) its first column relative to
-  // its tile (one division each, here, not per step)
+  const rsrc_t rm = mask_rsrc(p, ti.b);
+  // Each thread's chunks, the same in every step: window slot t, row offset
+  // and column within the tile (one division each, here, not per step)
   int tj[NL];
   uint32_t roff[NL];
-  int cofs[UNALIGNED ? NL : 1];
 #pragma unroll
   for (int n = 0; n < NL; ++n) {
     const int c = n * NT + tid, t = c / cpt, rem = c - t * cpt;
     tj[n] = t;
-    if constexpr (UNALIGNED) {
-      const int r = rem / cpr, k = rem - r * cpr;
-      const uint32_t rowb = base_mod + (uint32_t)(ti.m0 + r) * (uint32_t)p.m_rs * 2u;
-      const uint32_t sh = rowb & 15u;      // the row's first entry, bytes past a boundary
-      roff[n] = rowb - sh + 16u * (uint32_t)k;
-      cofs[n] = 8 * k - (int)(sh >> 1);
-    } else {
-      roff[n] = ((uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u) * 2u;
-    }
+    roff[n] = (uint32_t)(ti.m0 + (rem >> 3)) * (uint32_t)p.m_rs + (uint32_t)(rem & 7) * 8u;
   }
-  const int c0 = (tid & 7) * 8;   // aligned rows: NT and cpt are multiples of 8, rem & 7 == tid & 7
+  const int c0 = (tid & 7) * 8;   // NT and cpt are multiples of 8: rem & 7 == tid & 7
   const int sk = p.sk;
-  auto live = [&](u32x4 v, int n, int tile) -> bool {
-    if constexpr (UNALIGNED) return live8a<BF16>(v, cofs[n], tile * kBN, sk);
-    else return live8<BF16>(v, tile * kBN + c0, sk);
-  };
   int L = 0, R = nn - 1;
   for (int step = 0; lo < 0 || hi < 0; ++step) {
     if (L > R) break;                      // every tile scanned and dead
@@ -565,15 +521,15 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
 #pragma unroll
     for (int n = 0; n < NL; ++n) {
       const int t = tj[n];
-      va[n] = bload16(rm, roff[n] + (uint32_t)(t < ua ? a0 + da * t : L) * (kBN * 2u));
-      vb[n] = bload16(rm, roff[n] + (uint32_t)(t < ub ? b0 + db * t : L) * (kBN * 2u));
+      va[n] = bload16(rm, (roff[n] + (uint32_t)(t < ua ? a0 + da * t : L) * kBN) * 2u);
+      vb[n] = bload16(rm, (roff[n] + (uint32_t)(t < ub ? b0 + db * t : L) * kBN) * 2u);
     }
 #pragma unroll
     for (int n = 0; n < NL; ++n) {
       const int t = tj[n];
       const uint32_t bit = 1u << (t & 31);
-      abits |= ((t < ua) & live(va[n], n, a0 + da * t)) ? bit : 0u;
-      bbits |= ((t < ub) & live(vb[n], n, b0 + db * t)) ? bit : 0u;
+      abits |= ((t < ua) & live8<BF16>(va[n], (a0 + da * t) * kBN + c0, sk)) ? bit : 0u;
+      bbits |= ((t < ub) & live8<BF16>(vb[n], (b0 + db * t) * kBN + c0, sk)) ? bit : 0u;
     }
     wg_or2<NT>(abits, bbits, red, step & 1);
     if (both) {
@@ -592,9 +548,6 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   __syncthreads();                         // every wave has read `red` before any DMA lands
   // no visible entry in these rows: an empty range (lo = 0, hi = -1)
   if (lo < 0) { lo = 0; hi = -1; }
-#if MI355_SCAN_TIMING
-  if (lo <= hi) return false;   // timing only: the scan runs, the nominal ranges stand
-#endif
   const int ns = uni(p.num_splits);
   const int per = (hi - lo + 1 + ns - 1) / ns;
   const int nb = min(lo + ti.split * per, hi + 1);
@@ -1350,7 +1303,7 @@ void fa_fwd_kernel(const KParams p) {
   {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
-    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, false>(tn, p, G::kBM / p.pack, lp,
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true>(tn, p, G::kBM / p.pack, lp,
                                                        reinterpret_cast<uint32_t*>(KS(NST - 1)))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
@@ -1490,7 +1443,7 @@ void fa_fwd_kernel_asm(const KParams p) {
     // before the set-up below: its values would be live across the scan, and
     // the registers the scan needs on top of them would spill
     const LiveProbe lp = live_probe<64 * WAVES>(ti, p);
-    narrow_to_live<BF16, 64 * WAVES, 256, 4, false, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kAsmMBase));
+    narrow_to_live<BF16, 64 * WAVES, 256, 4, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kAsmMBase));
   }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1658,7 +1611,7 @@ void fa_fwd_kernel_pp(const KParams p) {
     // before the set-up below: its values would be live across the scan, and
     // the SGPRs the scan needs on top of them would spill
     const LiveProbe lp = live_probe<512>(ti, p);
-    narrow_to_live<true, 512, 256, 4, false, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kPpMBase));
+    narrow_to_live<true, 512, 256, 4, false>(ti, p, 256 / p.pack, lp, reinterpret_cast<uint32_t*>(smem + kPpMBase));
   }
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
