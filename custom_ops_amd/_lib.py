@@ -43,7 +43,8 @@ class Variant(ctypes.Structure):
     see the header for the meaning of each value."""
 
     _fields_ = [(name, ctypes.c_int32) for name in
-                ("waves", "pack", "order", "loop", "fuse", "live", "deep", "mask_mfma", "stream")]
+                ("waves", "pack", "order", "loop", "fuse", "live", "deep", "mask_mfma", "stream",
+                 "live_map")]
 
     def __repr__(self) -> str:
         set_ = {n: getattr(self, n) for n, _ in self._fields_ if getattr(self, n)}

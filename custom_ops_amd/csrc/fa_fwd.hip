@@ -205,6 +205,14 @@ struct KParams {
   // K/V tiles are read by exactly one workgroup each: the compiled kernel
   // streams them with the non-temporal hint
   int kv_nt;
+  // Live-tile map written by live_map_kernel before this launch (or null):
+  // bit t of byte (b·num_m + m-block)·map_row_bytes + t/8 is set when tile t
+  // holds a visible entry of the m-block's rows. With it the workgroups read
+  // their live ranges instead of scanning the mask.
+  const uint8_t* live_map;
+  int map_row_bytes;
+  int map_rows;              // rows per m-block (BM / pack)
+  uint8_t* live_map_out;     // the same map, for live_map_kernel
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -416,21 +424,23 @@ __device__ __forceinline__ bool live8(u32x4 v, int c0, int sk) {
   return any;
 }
 
-// OR over the workgroup: within each 16-lane row by DPP, over the wave's four
-// rows by readlane, then one word per wave in LDS (set `set` of two), read by
-// every thread after a barrier
+// OR over the wave: within each 16-lane row by DPP, over the four rows by
+// readlane (a uniform result)
+__device__ __forceinline__ uint32_t wave_or(uint32_t x) {
+  x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);    // quad_perm 1,0,3,2
+  x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);    // quad_perm 2,3,0,1
+  x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x124, 0xF, 0xF, false);   // row_ror 4
+  x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, false);   // row_ror 8
+  return __builtin_amdgcn_readlane(x, 0) | __builtin_amdgcn_readlane(x, 16) |
+         __builtin_amdgcn_readlane(x, 32) | __builtin_amdgcn_readlane(x, 48);
+}
+
+// OR over the workgroup: wave_or, then one word per wave in LDS (set `set` of
+// two), read by every thread after a barrier
 template <int NT>
 __device__ __forceinline__ void wg_or2(uint32_t& a, uint32_t& b, uint32_t* red, int set) {
   constexpr int kW = NT / 64;
-  auto row_or = [](uint32_t x) {
-    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);    // quad_perm 1,0,3,2
-    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);    // quad_perm 2,3,0,1
-    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x124, 0xF, 0xF, false);   // row_ror 4
-    x |= (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, false);   // row_ror 8
-    return __builtin_amdgcn_readlane(x, 0) | __builtin_amdgcn_readlane(x, 16) |
-           __builtin_amdgcn_readlane(x, 32) | __builtin_amdgcn_readlane(x, 48);
-  };
-  const uint32_t wa = row_or(a), wb = row_or(b);
+  const uint32_t wa = wave_or(a), wb = wave_or(b);
   const int tid = threadIdx.x;
   uint32_t* w = red + 2 * kW * set;
   w[tid >> 6] = wa;
@@ -450,11 +460,14 @@ __device__ __forceinline__ rsrc_t mask_rsrc(CKParams& p, int b) {
 
 struct LiveProbe { u32x4 l, r; };
 
-template <int NT>
+template <int NT, bool MAP = false>
 __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams& pk) {
   CKParams& p = kernarg_params(pk);
   LiveProbe pr{};
   if (!uni(p.live)) return pr;
+  if constexpr (MAP) {
+    if (p.live_map) return pr;
+  }
   const rsrc_t rm = mask_rsrc(p, ti.b);
   const int tid = threadIdx.x;
   const uint32_t rowoff = (uint32_t)(ti.m0 + (tid >> 3)) * (uint32_t)p.m_rs + (uint32_t)(tid & 7) * 8u;
@@ -463,7 +476,126 @@ __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams
   return pr;
 }
 
-template <bool BF16, int NT, int BMAX, int J, bool REUSE>
+// The live range of the workgroup's row block from the live-tile map: the
+// first and the last set bit of its row of the map (the same [lo, hi] the
+// scan below finds, so the same split ranges and the same results).
+template <int NT>
+__device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int rows, uint32_t* red) {
+  const int tid = threadIdx.x;
+  const int nbytes = uni(p.map_row_bytes);
+  const uint8_t* row = p.live_map + ((int64_t)ti.b * p.num_m + ti.m0 / rows) * nbytes;
+  if (tid == 0) { red[0] = 0x7fffffffu; red[1] = 0u; }
+  __syncthreads();
+  for (int i = tid; i < nbytes; i += NT) {
+    const uint32_t v = row[i];
+    if (v) {
+      atomicMin(reinterpret_cast<int*>(red), i * 8 + __builtin_ctz(v));
+      atomicMax(reinterpret_cast<int*>(red + 1), i * 8 + 32 - __builtin_clz(v));   // one past the last
+    }
+  }
+  __syncthreads();
+  int lo = (int)__builtin_amdgcn_readfirstlane(red[0]), hi = (int)__builtin_amdgcn_readfirstlane(red[1]) - 1;
+  __syncthreads();                         // every wave has read `red` before any DMA lands
+  if (lo > hi) { lo = 0; hi = -1; }        // no visible entry in these rows
+  if (lo == 0 && hi == p.num_n - 1) return false;   // whole axis live: the nominal ranges stand
+  const int ns = uni(p.num_splits);
+  const int per = (hi - lo + 1 + ns - 1) / ns;
+  const int nb = min(lo + ti.split * per, hi + 1);
+  ti.nb = nb;
+  ti.ne = min(nb + per, hi + 1);
+  return true;
+}
+
+// Live-tile map of a launch whose mask rows are not 16-byte aligned (a mask
+// of Sk % 8 != 0 columns): one workgroup per (batch, m-block, 8 KV tiles)
+// writes the map byte of those tiles, bit t set when tile t has an entry that
+// is not -inf in a column < Sk of a row < Sq of the m-block. The launch's
+// workgroups then read their live ranges from the map (range_from_map)
+// instead of each scanning its rows' mask: the rows of an m-block are shared
+// by every head group and split of it (8 workgroups on cfg5's shape), which
+// each read its dead mask once more, and the scan's 16-byte loads of
+// unaligned rows run at a fraction of the aligned rate. Here every chunk is an
+// aligned 16-byte load: a row that starts sh bytes past a 16-byte boundary
+// is read from that boundary, and each entry is attributed to its own tile
+// by its column. Every map byte is written by exactly one workgroup, so the
+// map needs no clearing.
+template <bool BF16>
+__global__ __launch_bounds__(256) void live_map_kernel(KParams p) {
+  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u;
+  constexpr int kThreads = 256;
+  const int g = blockIdx.x % p.map_row_bytes;          // 8-tile group
+  const int rb = (blockIdx.x / p.map_row_bytes) % p.num_m;
+  const int b = blockIdx.x / (p.map_row_bytes * p.num_m);
+  const int m0 = rb * p.map_rows;
+  const int nr = min(p.map_rows, p.sq - m0);
+  const uint16_t* mb = p.mask + (int64_t)b * p.m_bs;
+  const uint32_t base_mod = (uint32_t)reinterpret_cast<uintptr_t>(mb) & 15u;
+  const rsrc_t rm = make_rsrc(reinterpret_cast<const uint8_t*>(mb) - base_mod,
+                              (uint32_t)p.msq * p.m_rs * 2u + base_mod);
+  const int c_lo = g * 8 * kBN, c_hi = min(c_lo + 8 * kBN, p.sk);   // columns of this group, < Sk
+  __shared__ uint32_t bits;
+  if (threadIdx.x == 0) bits = 0u;
+  __syncthreads();
+  const uint32_t full = (1u << ((c_hi - c_lo + kBN - 1) / kBN)) - 1u;   // every tile of the group live
+  uint32_t mine = 0u;
+  // per row: the aligned chunks covering columns c_lo .. c_hi - 1; each
+  // thread issues kBatch loads before it looks at any (one memory round trip
+  // per batch), then classifies each chunk's 8 entries with word operations
+  // (256 threads and batches of 4: the fastest of the shapes tried, 5-6 µs
+  // on cfg5's 16 MB mask)
+  constexpr int kBatch = 4;
+  const int cpr = (c_hi - c_lo + 7) / 8 + 1;
+  const int total = nr * cpr;
+  for (int c0 = 0; c0 < total; c0 += kThreads * kBatch) {
+    u32x4 v[kBatch];
+    int col0[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int c = c0 + u * kThreads + (int)threadIdx.x;
+      const int r = c / cpr, j = c - r * cpr;
+      const uint32_t rowb = base_mod + ((uint32_t)(m0 + r) * (uint32_t)p.m_rs + (uint32_t)c_lo) * 2u;
+      const uint32_t sh = rowb & 15u;
+      // past the last chunk: an out-of-range offset, which reads 0 without an access
+      v[u] = bload16(rm, c < total ? rowb - sh + 16u * (uint32_t)j : 0xfffffff0u);
+      col0[u] = c < total ? c_lo + 8 * j - (int)(sh >> 1) : c_hi;   // column of the chunk's first entry
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      // entries that are not -inf, one bit each
+      uint32_t vis = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vis |= ((v[u][i] & 0xffffu) != kNeg ? 1u : 0u) << (2 * i);
+        vis |= ((v[u][i] >> 16) != kNeg ? 1u : 0u) << (2 * i + 1);
+      }
+      // entries inside [c_lo, c_hi)
+      const int lo = c_lo - col0[u], hi = c_hi - col0[u];       // entry range e in [lo, hi)
+      const uint32_t in = (lo >= 8 || hi <= 0) ? 0u
+                          : ((0xffu << max(lo, 0)) & (0xffu >> (8 - min(hi, 8)))) & 0xffu;
+      vis &= in;
+      if (vis) {
+        // the chunk's entries fall in at most two tiles: those before the
+        // first tile boundary in it, then the rest
+        const int t0 = (max(col0[u], c_lo) - c_lo) / kBN;
+        const int split = (t0 + 1) * kBN + c_lo - col0[u];         // first entry of tile t0 + 1
+        const uint32_t first = split >= 8 ? 0xffu : (0xffu >> (8 - max(split, 0)));
+        if (vis & first) mine |= 1u << t0;
+        if (vis & ~first & 0xffu) mine |= 2u << t0;
+      }
+    }
+    // once every tile of the group is known live (a dense mask: after the
+    // first batch) the rest need not be read
+    mine = wave_or(mine);   // one LDS atomic per wave, not per thread
+    if ((threadIdx.x & 63) == 0 && mine) atomicOr(&bits, mine);
+    __syncthreads();
+    if (bits == full) break;
+    __syncthreads();        // every wave has read `bits` before the next batch's atomics
+  }
+  if (threadIdx.x == 0)
+    p.live_map_out[((int64_t)b * p.num_m + rb) * p.map_row_bytes + g] = (uint8_t)bits;
+}
+
+template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool MAP = false>
 __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, int rows, const LiveProbe& pr,
                                                uint32_t* red) {
   CKParams& p = kernarg_params(pk);
@@ -472,6 +604,9 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   if (nr <= 0) return false;
   const int tid = threadIdx.x;
   const int nn = p.num_n;   // the scan's control stays in VGPRs: no SGPRs to spare here
+  if constexpr (MAP) {
+    if (p.live_map) return range_from_map<NT>(ti, p, rows, red);
+  }
   // the probe's verdict: tile 0 / tile nn - 1 live in the chunks it read
   uint32_t lb = ((tid < nr * 8) & live8<BF16>(pr.l, (tid & 7) * 8, p.sk)) ? 1u : 0u;
   uint32_t rb = ((tid < nr * 8) & live8<BF16>(pr.r, (nn - 1) * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
@@ -1268,7 +1403,7 @@ void fa_fwd_kernel(const KParams p) {
 
   TileIdx ti = tile_index<G::kBM>(p);
   const TileIdx tg = ti;   // the workgroup's first head and row
-  const LiveProbe lp = live_probe<G::kThreads>(tg, p);
+  const LiveProbe lp = live_probe<G::kThreads, !MDIRECT>(tg, p);
   place_wave(ti, p, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), 32);
   A a(p);
   a.init(ti);
@@ -1303,7 +1438,7 @@ void fa_fwd_kernel(const KParams p) {
   {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
-    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true>(tn, p, G::kBM / p.pack, lp,
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, !MDIRECT>(tn, p, G::kBM / p.pack, lp,
                                                        reinterpret_cast<uint32_t*>(KS(NST - 1)))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
@@ -1948,6 +2083,9 @@ struct Plan {
   int live;
   int mask_mfma_off;   // the compiled kernel widens bf16 masks on the VALU
   int kv_nt;           // every K/V tile is read by one workgroup: non-temporal loads
+  int live_map;        // a live-tile map pre-pass serves the live ranges (unaligned mask rows)
+  int map_row_bytes;
+  size_t map_bytes;
 };
 
 // Tile plan: the workgroup size (4 or 8 waves) and split count with the
@@ -2068,15 +2206,25 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
     pl.fuse = s <= kFuseMaxSplits && pl.o_part_bytes < (1ull << 31) && pl.lse_bytes < (1ull << 31) &&
               v.fuse >= 0;
   }
-  pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
+  pl.loop = v.loop < 0 ? 0 : (v.loop >= 1 && v.loop <= 3 ? v.loop : 3);
+  pl.live = v.live < 0 ? 0 : (v.live > 0 ? 1 : 2);
+  // Masks whose rows are not 16-byte aligned run the compiled kernel, which
+  // narrows every launch (live on); their live ranges come from a pre-pass
+  // map instead of each workgroup's scan.
+  {
+    const bool mask_direct = ((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
+                             (p->mask_row_stride & 7) == 0;
+    pl.live_map = !mask_direct && pl.live != 0 && pl.num_n >= 4 && v.live_map >= 0;
+    pl.map_row_bytes = ceil_div(pl.num_n, 8);
+    pl.map_bytes = pl.live_map ? (((size_t)p->b * pl.num_m * pl.map_row_bytes + 255) & ~(size_t)255) : 0;
+  }
+  pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes + pl.map_bytes;
   // A 4-wave grid that puts at most one workgroup on each CU takes a third K/V
   // stage (112 KiB of LDS at d = 128: one workgroup per CU; cfg4 cold -7 %).
   {
     const int64_t wgs = (int64_t)p->b * (p->h / pl.pack) * pl.num_m * s;
     pl.deep = (pl.waves == 4 && wgs <= cus && v.deep >= 0) ? 1 : 0;
   }
-  pl.loop = v.loop < 0 ? 0 : (v.loop >= 1 && v.loop <= 3 ? v.loop : 3);
-  pl.live = v.live < 0 ? 0 : (v.live > 0 ? 1 : 2);
   pl.mask_mfma_off = v.mask_mfma < 0 ? 1 : 0;
   // One m-block per head group and every q-head of a KV head in the same
   // workgroup: each K/V tile is read by exactly one workgroup of the launch
@@ -2201,6 +2349,13 @@ static hipError_t launch(const KParams& kp_in, const CParams& cp, const Plan& pl
   KParams kp = kp_in;
   const int lm = pl.live;
   kp.live = pl.num_n >= 4 && (lm == 1 || (lm == 2 && (pl.splits > 1 || !runs_asm_loop<D, BF16>(kp, pl))));
+  if (kp.live && kp.live_map_out) {
+    hipLaunchKernelGGL((live_map_kernel<BF16>), dim3((unsigned)(kp.b * kp.num_m * kp.map_row_bytes)), dim3(256), 0,
+                       st, kp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    kp.live_map = kp.live_map_out;
+  }
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
   // the fused tail is in the compiled kernel only (the assembly loops keep no
   // registers for it): their split launches keep the combine launch
@@ -2280,9 +2435,9 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
     }
   }
   const bool split = pl.splits > 1;
-  if (split && (!p->workspace || p->workspace_bytes < pl.ws_bytes)) {
-    set_err(err, errlen, "split-KV needs %zu workspace bytes, got %zu", pl.ws_bytes,
-            p->workspace_bytes);
+  if (pl.ws_bytes && (!p->workspace || p->workspace_bytes < pl.ws_bytes)) {
+    set_err(err, errlen, "%s needs %zu workspace bytes, got %zu",
+            split ? "split-KV" : "the live-tile map", pl.ws_bytes, p->workspace_bytes);
     return MI355_FA_EWORKSPACE;
   }
 
@@ -2313,6 +2468,13 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.head_major = pl.head_major;
   kp.mask_direct = (((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
                     (p->mask_row_stride & 7) == 0) ? 1 : 0;
+
+  if (pl.live_map) {
+    uint8_t* map = (uint8_t*)p->workspace + pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
+    kp.live_map_out = map;
+    kp.map_row_bytes = pl.map_row_bytes;
+    kp.map_rows = pl.block_m / pl.pack;
+  }
 
   CParams cp{};
   if (split) {

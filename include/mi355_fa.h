@@ -64,6 +64,8 @@ typedef struct mi355_fa_variant {
   int32_t stream;    /* 0 | 1 on | -1 off: the compiled kernel loads K/V with the
                         non-temporal hint (default: when each K/V tile is read by
                         one workgroup of the launch)                               */
+  int32_t live_map;  /* 0 | -1: masks with unaligned rows narrow by each workgroup's
+                        own scan instead of the live-tile map pre-pass             */
 } mi355_fa_variant;
 
 /*
@@ -100,8 +102,9 @@ typedef struct mi355_fa_params {
 
   /* Split-KV: 0 = let the library plan it; >= 1 forces that many splits. */
   int32_t num_splits;
-  /* Device workspace for split-KV partials and the fused split tail's ticket
-   * words (may be NULL when no split is planned; its contents need no clearing). */
+  /* Device workspace for split-KV partials, the fused split tail's ticket
+   * words and the live-tile map of masks with unaligned rows (may be NULL when
+   * mi355_fa_workspace_bytes reports 0; its contents need no clearing). */
   void* workspace;
   size_t workspace_bytes;
   /* Test/tuning variant selection (NULL = the library's plan); see above. */
@@ -116,7 +119,8 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
 #define MI355_FA_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20) /* 32 MiB */
 
 /* mi355_fa_fwd without any allocation and without a workspace argument: the
- * split-KV partials go to a fixed per-GPU device array of
+ * workspace contents (split-KV partials and tickets, the live-tile map of
+ * masks with unaligned rows) go to a fixed per-GPU device array of
  * MI355_FA_NOALLOC_SCRATCH_BYTES (allocated when the library's code is loaded
  * onto a GPU and held until the process ends). p->workspace is ignored. Plans
  * that need more scratch fail with MI355_FA_EWORKSPACE. Calls that overlap on
@@ -130,7 +134,8 @@ int mi355_fa_fwd_noalloc(const mi355_fa_params* p, void* stream, char* err, size
  * the MI355_FA_NUM_SPLITS override, read once per process, and clamping). */
 int mi355_fa_num_splits(const mi355_fa_params* p);
 
-/* Bytes of workspace mi355_fa_fwd needs for these params (0 when unsplit). */
+/* Bytes of workspace mi355_fa_fwd needs for these params (split partials and
+ * tickets, the live-tile map of masks with unaligned rows; 0 when neither). */
 size_t mi355_fa_workspace_bytes(const mi355_fa_params* p);
 
 /* Pure cost model, exposed for host tests: splits for a problem of

@@ -449,14 +449,16 @@ def test_moving_running_max(ops, gpu, slope, splits):
 @pytest.mark.parametrize("shape,splits", [((1, 4, 2, 200, 3000, 128), 0),   # auto: split
                                           ((2, 4, 4, 300, 700, 64), 1),    # unsplit
                                           ((1, 4, 2, 200, 3001, 128), 2),  # compiled kernel, fused tail
-                                          ((1, 4, 2, 200, 3001, 128), 5)])  # compiled kernel, combine
+                                          ((1, 4, 2, 200, 3001, 128), 5),  # compiled kernel, combine
+                                          ((2, 4, 4, 300, 777, 128), 1)])  # unsplit, live-tile map
 def test_graph_capture_replays(ops, gpu, shape, splits):
     """The op captured in a HIP graph (workspace from the graph-aware caching
     allocator, no memset nodes) and replayed several times with new inputs
     copied into the captured buffers, eager work and synchronisations in
     between: every replay equals the eager result bit for bit. A replay reuses
     the captured launch tag and its own workspace, so the fused tail's ticket
-    words count on across replays."""
+    words count on across replays; masks with unaligned rows replay the
+    live-tile map kernel before the attention kernel."""
     from custom_ops_amd import mha_fwd_with_mask
     b, h, hk, sq, sk, d = shape
     q, k, v, m = (t.to(gpu) for t in make_case(b, h, hk, sq, sk, d, "inf_random",

@@ -1,14 +1,18 @@
 """Live-range narrowing (each workgroup runs only the KV tiles from the first to
 the last one in which its rows' mask has a visible entry, and the splits share
 that range): parity on masks with dead edges, for every tile-loop form, with
-narrowing forced on (``Variant(live=1)``) and off (``live=-1``).
+narrowing forced on (``Variant(live=1)``) and off (``live=-1``), and, for
+masks whose rows are not 16-byte aligned, the live ranges from the pre-pass
+live-tile map against each workgroup's own scan (``live_map=-1``).
 
   * every output against the fp32 torch restatement of the reference op
     (tests/test_mha_fwd_with_mask.py:38-53 of the reference) at the suite's
     tolerance, fully masked rows exactly 0;
   * unsplit launches: narrowed == not narrowed, bit for bit (a tile whose
     scores are all -inf leaves O, l and the running max unchanged);
-  * split launches re-partition the live range, so only the tolerance holds.
+  * split launches re-partition the live range, so only the tolerance holds;
+  * the live-tile map (exact ranges) and the scan (ranges that may be wider):
+    bit for bit when unsplit, within the tolerance when split.
 
 Cases: causal, sliding window, leading + trailing key padding, an m-block
 whose rows are all masked, only the last (ragged) tile live, only key 0 live,
@@ -76,6 +80,15 @@ CASES = [  # kind, b, h, hk, sq, sk, d, dtype, splits (0: the plan's), extra mas
     ("window", 1, 4, 4, 512, 2048, 128, torch.float16, 1, 0, 0),
     ("window", 1, 4, 4, 512, 2048, 64, torch.bfloat16, 1, 0, 0),
     ("causal", 1, 4, 2, 512, 512, 64, torch.float16, 2, 0, 0),
+    # rows not 16-byte aligned (the live-tile map): trap columns, rows past
+    # Sq, fp16, d = 64, and batch 1's mask starting off a 16-byte boundary
+    ("trap_cols", 1, 2, 2, 256, 1030, 128, torch.bfloat16, 1, 3, 0),
+    ("rows_past_sq", 1, 2, 2, 200, 1021, 128, torch.bfloat16, 2, 0, 56),
+    ("window", 1, 4, 4, 512, 2051, 128, torch.float16, 1, 0, 0),
+    ("window", 1, 4, 4, 512, 2051, 64, torch.bfloat16, 3, 0, 0),
+    ("pad", 1, 4, 1, 300, 3001, 128, torch.bfloat16, 5, 0, 0),
+    ("window", 2, 4, 2, 301, 777, 128, torch.bfloat16, 0, 0, 0),
+    ("causal", 2, 4, 2, 301, 777, 128, torch.bfloat16, 3, 0, 0),
 ]
 
 
@@ -84,6 +97,7 @@ CASES = [  # kind, b, h, hk, sq, sk, d, dtype, splits (0: the plan's), extra mas
 def test_live_range_parity(gpu, loop):
     from custom_ops_amd import Variant, mha_fwd_with_mask
     on, off = Variant(loop=loop, live=1), Variant(loop=loop, live=-1)
+    scan = Variant(loop=loop, live=1, live_map=-1)   # unaligned rows: the scan instead of the map
     for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr) in enumerate(CASES):
         g = torch.Generator().manual_seed(1000 + n)
         q = (torch.randn(b, h, sq, d, generator=g) * 0.5).to(dt).cuda()
@@ -92,9 +106,16 @@ def test_live_range_parity(gpu, loop):
         m = mask_of(kind, b, sq, sk, sk + xc, sq + xr, g).to(dt).cuda()
         ref = ref_attn_torch(q, k, v, m[:, :, :sq, :sk])
         dead = torch.isinf(m[:, :, :sq, :sk].float()).all(-1)          # [b, 1, sq]
-        outs = [mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=var) for var in (on, off)]
+        outs = [mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=var) for var in (on, off, scan)]
         torch.cuda.synchronize()
-        for var, out in zip(("on", "off"), outs):
+        # Unsplit, the map's exact range and the scan's (which may be wider: a
+        # chunk read partly past the end of the mask counts as visible) give
+        # the same bits, since dead tiles add nothing; split launches then
+        # partition different ranges, so only the tolerance holds.
+        if splits == 1:
+            assert torch.equal(outs[0].view(torch.int16), outs[2].view(torch.int16)), \
+                f"loop {loop} case {n} {kind}: live-tile map and scan differ"
+        for var, out in zip(("on", "off", "scan"), outs):
             tag = f"loop {loop} live {var} case {n} {kind}"
             assert_close(out, ref, tag)
             assert bool((out.float().masked_select(dead.unsqueeze(-1).expand(b, h, sq, d)) == 0).all()), tag

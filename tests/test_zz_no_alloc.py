@@ -1,4 +1,5 @@
-"""mi355_fa_fwd_noalloc (split partials in the library's per-GPU scratch array,
+"""mi355_fa_fwd_noalloc (split partials and the live-tile map of masks with
+unaligned rows in the library's per-GPU scratch array,
 no workspace, no allocation) against mi355_fa_fwd with a caller workspace, both
 called through the C-ABI: bit-identical outputs on two calls in a row (the
 second smaller, so stale scratch contents from the first must not leak in),
@@ -58,6 +59,8 @@ def test_noalloc_matches_workspace_entry_two_calls(dtype):
         # the second is smaller and reuses it
         (1, 16, 16, 128, 16384, 128, 16, 11),
         (1, 4, 2, 100, 3001, 64, 5, 12),
+        # unsplit, unaligned mask rows: only the live-tile map in the array
+        (2, 4, 4, 300, 777, 128, 1, 13),
     ]
     for b, h, hk, sq, sk, d, splits, seed in cases:
         q, k, v, mask = _inputs(b, h, hk, sq, sk, d, seed, dtype)
@@ -69,7 +72,7 @@ def test_noalloc_matches_workspace_entry_two_calls(dtype):
 
 
 def test_noalloc_unsplit_needs_no_scratch():
-    q, k, v, mask = _inputs(2, 4, 4, 300, 777, 128, 13)
+    q, k, v, mask = _inputs(2, 4, 4, 300, 776, 128, 13)
     ref, need = _run("fwd", q, k, v, mask, 1)
     got, _ = _run("noalloc", q, k, v, mask, 1)
     assert need == 0
