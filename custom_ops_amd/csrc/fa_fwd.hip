@@ -513,75 +513,49 @@ __device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int row
 // workgroups then read their live ranges from the map (range_from_map)
 // instead of each scanning its rows' mask: the rows of an m-block are shared
 // by every head group and split of it (8 workgroups on cfg5's shape), which
-// each read its dead mask once more, and the scan's 16-byte loads of
-// unaligned rows run at a fraction of the aligned rate. Here every chunk is an
-// aligned 16-byte load: a row that starts sh bytes past a 16-byte boundary
-// is read from that boundary, and each entry is attributed to its own tile
-// by its column. Every map byte is written by exactly one workgroup, so the
+// would each read its dead mask once more. A lane reads 16 bytes = 8 entries
+// of one row (8 lanes per tile row, the chunks of the scan, unaligned loads
+// cost no more here than aligned ones): a chunk below Sk is live unless its
+// four words are all the -inf pair, and only the chunk that holds Sk checks
+// entry by entry. Every map byte is written by exactly one workgroup, so the
 // map needs no clearing.
 template <bool BF16>
 __global__ __launch_bounds__(256) void live_map_kernel(KParams p) {
-  constexpr uint32_t kNeg = BF16 ? 0xff80u : 0xfc00u;
-  constexpr int kThreads = 256;
+  constexpr uint32_t kNegPair = BF16 ? 0xff80ff80u : 0xfc00fc00u;
+  constexpr int kThreads = 256, kBatch = 4, kChunksPerRow = 8 * 8;   // 8 tiles x 8 chunks
   const int g = blockIdx.x % p.map_row_bytes;          // 8-tile group
   const int rb = (blockIdx.x / p.map_row_bytes) % p.num_m;
   const int b = blockIdx.x / (p.map_row_bytes * p.num_m);
   const int m0 = rb * p.map_rows;
   const int nr = min(p.map_rows, p.sq - m0);
-  const uint16_t* mb = p.mask + (int64_t)b * p.m_bs;
-  const uint32_t base_mod = (uint32_t)reinterpret_cast<uintptr_t>(mb) & 15u;
-  const rsrc_t rm = make_rsrc(reinterpret_cast<const uint8_t*>(mb) - base_mod,
-                              (uint32_t)p.msq * p.m_rs * 2u + base_mod);
+  const rsrc_t rm = make_rsrc(p.mask + (int64_t)b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
   const int c_lo = g * 8 * kBN, c_hi = min(c_lo + 8 * kBN, p.sk);   // columns of this group, < Sk
+  const uint32_t full = (1u << ((c_hi - c_lo + kBN - 1) / kBN)) - 1u;   // every tile of the group live
   __shared__ uint32_t bits;
   if (threadIdx.x == 0) bits = 0u;
   __syncthreads();
-  const uint32_t full = (1u << ((c_hi - c_lo + kBN - 1) / kBN)) - 1u;   // every tile of the group live
-  uint32_t mine = 0u;
-  // per row: the aligned chunks covering columns c_lo .. c_hi - 1; each
-  // thread issues kBatch loads before it looks at any (one memory round trip
-  // per batch), then classifies each chunk's 8 entries with word operations
-  // (256 threads and batches of 4: the fastest of the shapes tried, 5-6 µs
-  // on cfg5's 16 MB mask)
-  constexpr int kBatch = 4;
-  const int cpr = (c_hi - c_lo + 7) / 8 + 1;
-  const int total = nr * cpr;
-  for (int c0 = 0; c0 < total; c0 += kThreads * kBatch) {
+  const int total = nr * kChunksPerRow;
+  for (int base = 0; base < total; base += kThreads * kBatch) {
     u32x4 v[kBatch];
-    int col0[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int c = c0 + u * kThreads + (int)threadIdx.x;
-      const int r = c / cpr, j = c - r * cpr;
-      const uint32_t rowb = base_mod + ((uint32_t)(m0 + r) * (uint32_t)p.m_rs + (uint32_t)c_lo) * 2u;
-      const uint32_t sh = rowb & 15u;
-      // past the last chunk: an out-of-range offset, which reads 0 without an access
-      v[u] = bload16(rm, c < total ? rowb - sh + 16u * (uint32_t)j : 0xfffffff0u);
-      col0[u] = c < total ? c_lo + 8 * j - (int)(sh >> 1) : c_hi;   // column of the chunk's first entry
+      const int c = base + u * kThreads + (int)threadIdx.x;
+      const int c0 = c_lo + 8 * (c & (kChunksPerRow - 1));
+      const bool in = c < total && c0 < c_hi;
+      // outside: an out-of-range offset, which reads 0 without an access
+      v[u] = bload16(rm, in ? ((uint32_t)(m0 + (c >> 6)) * (uint32_t)p.m_rs + (uint32_t)c0) * 2u
+                            : 0xfffffff0u);
     }
+    uint32_t mine = 0u;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      // entries that are not -inf, one bit each
-      uint32_t vis = 0u;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        vis |= ((v[u][i] & 0xffffu) != kNeg ? 1u : 0u) << (2 * i);
-        vis |= ((v[u][i] >> 16) != kNeg ? 1u : 0u) << (2 * i + 1);
-      }
-      // entries inside [c_lo, c_hi)
-      const int lo = c_lo - col0[u], hi = c_hi - col0[u];       // entry range e in [lo, hi)
-      const uint32_t in = (lo >= 8 || hi <= 0) ? 0u
-                          : ((0xffu << max(lo, 0)) & (0xffu >> (8 - min(hi, 8)))) & 0xffu;
-      vis &= in;
-      if (vis) {
-        // the chunk's entries fall in at most two tiles: those before the
-        // first tile boundary in it, then the rest
-        const int t0 = (max(col0[u], c_lo) - c_lo) / kBN;
-        const int split = (t0 + 1) * kBN + c_lo - col0[u];         // first entry of tile t0 + 1
-        const uint32_t first = split >= 8 ? 0xffu : (0xffu >> (8 - max(split, 0)));
-        if (vis & first) mine |= 1u << t0;
-        if (vis & ~first & 0xffu) mine |= 2u << t0;
-      }
+      const int c = base + u * kThreads + (int)threadIdx.x;
+      const int c0 = c_lo + 8 * (c & (kChunksPerRow - 1));
+      if (c >= total || c0 >= c_hi) continue;
+      bool live = !((v[u][0] == kNegPair) & (v[u][1] == kNegPair) & (v[u][2] == kNegPair) &
+                    (v[u][3] == kNegPair));
+      if (c0 + 8 > c_hi) live = live8<BF16>(v[u], c0, c_hi);   // the chunk that holds Sk
+      if (live) mine |= 1u << ((c & (kChunksPerRow - 1)) >> 3);
     }
     // once every tile of the group is known live (a dense mask: after the
     // first batch) the rest need not be read

@@ -62,9 +62,13 @@ STALL_PASSES = {
 }
 
 
+COLD = False   # --cold: every counted launch after a cache flush
+
+
 def workload_cmd(cfg: str, iters: int, bcast: bool = False) -> list[str]:
     return [sys.executable, "-m", "custom_ops_amd.prof_workload", "--config", cfg, "--iters",
-            str(iters), "--copy-mib", str(COPY_MIB), *(["--mask-bcast"] if bcast else [])]
+            str(iters), "--copy-mib", str(COPY_MIB), *(["--mask-bcast"] if bcast else []),
+            *(["--cold"] if COLD else [])]
 
 
 def rocprof_cmd(name: str, outdir: str, cfg: str, iters: int) -> list[str]:
@@ -105,6 +109,10 @@ def is_attn(name: str) -> bool:
 
 def is_combine(name: str) -> bool:
     return "fa_combine_kernel" in name
+
+
+def is_map(name: str) -> bool:
+    return "live_map_kernel" in name
 
 
 def is_copy(name: str) -> bool:
@@ -265,11 +273,15 @@ def main() -> None:
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--out", default=os.path.join(ROOT, "prof_out"))
     ap.add_argument("--stall", action="store_true", help="wave-state counters instead")
+    ap.add_argument("--cold", action="store_true",
+                    help="flush the caches before every counted launch (the bench's cold launches)")
     ap.add_argument("--bench", action="store_true", help="kernel trace of bench.py's timed run instead")
     ap.add_argument("--power", action="store_true", help="socket power and clocks per workload instead")
     ap.add_argument("--loop-s", type=float, default=10.0, help="--power: seconds per workload")
     args = ap.parse_args()
     args.out = os.path.abspath(args.out)      # the passes run with cwd=/tmp
+    global COLD
+    COLD = args.cold
     os.makedirs(args.out, exist_ok=True)
     sys.path.insert(0, ROOT)
     from custom_ops_amd.workloads import CONFIGS
@@ -292,6 +304,7 @@ def main() -> None:
         raise RuntimeError("no fa_fwd_kernel dispatch in the kernel trace")
     avg_ns = float(attn[0]["AverageNs"])
     comb = [r for r in stats if is_combine(r["Name"])]
+    lmap = [r for r in stats if is_map(r["Name"])]
 
     fetch_copy = counter_means(dirs["fetch"], is_copy).get("FETCH_SIZE")
     write_copy = counter_means(dirs["write"], is_copy).get("WRITE_SIZE")
@@ -303,9 +316,17 @@ def main() -> None:
     traffic = None
     if f_fac and w_fac:
         traffic = (fetch * f_fac + write * w_fac) * 1024
+    fetch_map = counter_means(dirs["fetch"], is_map).get("FETCH_SIZE")
+    fetch_comb = counter_means(dirs["fetch"], is_combine).get("FETCH_SIZE")
+    write_comb = counter_means(dirs["write"], is_combine).get("WRITE_SIZE")
     fetch_b = counter_means(dirs["fetch_bcast"], is_attn)["FETCH_SIZE"]
     mask_alg = cfg.B * cfg.Sq * cfg.Sk * 2
-    mask_counted = (fetch - fetch_b) * f_fac * 1024 if f_fac else None
+    # The broadcast call (mask strides 0) is a like-for-like comparison only
+    # when the mask's rows are 16-byte aligned already: with unaligned rows
+    # (Sk % 8 != 0) the strides-0 call takes the aligned mask path and skips
+    # the live-tile map, so the difference would not be the mask stream.
+    aligned = cfg.Sk % 8 == 0
+    mask_counted = (fetch - fetch_b) * f_fac * 1024 if (f_fac and aligned) else None
     mf = counter_means(dirs["mfma"], is_attn)
     ld = counter_means(dirs["lds"], is_attn)
     simds, xcds = 256 * 4, 8
@@ -315,7 +336,34 @@ def main() -> None:
     bank_conf = ld["SQ_LDS_BANK_CONFLICT"] / max(1.0, ld["SQ_LDS_IDX_ACTIVE"])
 
     kname = attn[0]["Name"]
-    stem = f"fa_fwd_kernel_{cfg.name}"
+    stem = f"fa_fwd_kernel_{cfg.name}" + ("_cold" if COLD else "")
+    # The counted launches are the last --iters of each kernel in the trace
+    # (the clock-settle launches come first): their mean duration, and for
+    # a launch sequence the mean of (end of its last kernel - start of the
+    # attention kernel), i.e. including the gap to a map / combine kernel.
+    trace = sorted(rows(dirs["trace"], "kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+
+    def counted(pred):
+        ds = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace if pred(r["Kernel_Name"])]
+        ds = ds[-args.iters:]
+        return sum(ds) / len(ds) if ds else None
+
+    ours = [r for r in trace if "mi355fa::" in r["Kernel_Name"]]
+    spans, i = [], 0
+    while i < len(ours):            # a call: [live_map] attention [combine]
+        j = i
+        while j < len(ours) and not is_attn(ours[j]["Kernel_Name"]):
+            j += 1
+        if j == len(ours):
+            break
+        start = int(ours[i]["Start_Timestamp"])
+        end = int(ours[j]["End_Timestamp"])
+        if j + 1 < len(ours) and is_combine(ours[j + 1]["Kernel_Name"]):
+            j += 1
+            end = int(ours[j]["End_Timestamp"])
+        spans.append((end - start) / 1e3)
+        i = j + 1
+    spans = spans[-args.iters:]
     mask_bytes = cfg.B * cfg.Sq * cfg.Sk * 2
     summary = {
         "config": cfg.name,
@@ -324,7 +372,16 @@ def main() -> None:
         "avg_duration_us": avg_ns / 1e3,
         "min_duration_us": float(attn[0]["MinNs"]) / 1e3,
         "max_duration_us": float(attn[0]["MaxNs"]) / 1e3,
+        "counted_launches": args.iters,
+        "counted_avg_us": counted(is_attn),
+        "counted_combine_avg_us": counted(is_combine) if comb else None,
+        "counted_live_map_avg_us": counted(is_map) if lmap else None,
+        "counted_call_span_us": sum(spans) / len(spans) if spans else None,
         "combine_avg_us": float(comb[0]["AverageNs"]) / 1e3 if comb else None,
+        "live_map_avg_us": float(lmap[0]["AverageNs"]) / 1e3 if lmap else None,
+        "live_map_fetch_bytes": fetch_map * f_fac * 1024 if (fetch_map and f_fac) else None,
+        "combine_bytes": ((fetch_comb or 0) * f_fac + (write_comb or 0) * w_fac) * 1024
+                         if (comb and f_fac and w_fac) else None,
         "achieved_tflops": cfg.flops / (avg_ns * 1e-9) / 1e12,
         "pct_bf16_peak": 100 * cfg.flops / (avg_ns * 1e-9) / 1e12 / 2500.0,
         "fetch_kib_raw": fetch, "write_kib_raw": write,
@@ -364,10 +421,12 @@ def main() -> None:
                              "strides 0 (custom_ops_amd.prof_collect)"}, f, indent=1)
     lines = [f"# rocprofv3 summary: fa_fwd_kernel on {cfg.name}", ""]
     lines.append(f"workload: {cfg.name} B={cfg.B} H={cfg.H} Hk={cfg.Hk} Sq={cfg.Sq} Sk={cfg.Sk} "
-                 f"d={cfg.d} bf16 ({cfg.description}); {args.iters} launches after clock settle")
+                 f"d={cfg.d} bf16 ({cfg.description}); {args.iters} launches after clock settle"
+                 + (", each after a 512 MiB zero + read-back (cold caches)" if COLD else ", back to back"))
     lines.append("")
     lines.append("commands (run from the repository root; each pass is its own process):")
-    lines.append(f"  python -m custom_ops_amd.prof_collect --config {cfg.name} --iters {args.iters}")
+    lines.append(f"  python -m custom_ops_amd.prof_collect --config {cfg.name} --iters {args.iters}"
+                 + (" --cold" if COLD else ""))
     for p in PASSES:
         lines.append("  cd /tmp && TMPDIR=/tmp PYTHONPATH=<repo> " +
                      " ".join(rocprof_cmd(p, f"<out>/raw/{p}", cfg.name, args.iters)))

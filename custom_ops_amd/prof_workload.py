@@ -16,6 +16,10 @@ differ (no tile of the cfg2/cfg3 masks is entirely -inf either way).
 --config instead and prints the achieved rate: the steady state in which
 socket power and clocks are sampled.
 
+--cold precedes every counted launch with a 512 MiB zero and read-back (the
+bench's cold, clean caches), so the kernel trace shows cold launches; without
+it the launches run back to back.
+
 Inputs are generated and copied to the GPU before any timed launch; the GPU
 clocks are settled first with untimed launches (--settle-s).
 """
@@ -34,6 +38,8 @@ def main() -> None:
                     help="mask row/batch strides 0: one L2-resident mask row for every query row")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run 5 copies of a buffer of this many MiB (read N, write N)")
+    ap.add_argument("--cold", action="store_true",
+                    help="flush the caches (512 MiB zero + read-back) before every counted launch")
     ap.add_argument("--loop-s", type=float, default=0.0,
                     help="run back to back for this many seconds and print the achieved rate")
     args = ap.parse_args()
@@ -82,7 +88,14 @@ def main() -> None:
         us = (time.perf_counter() - t0) / n * 1e6
         print(f"prof_workload {cfg.name}: loop {n} calls, {us:.2f} us/call", flush=True)
         return
+    flush = red = None
+    if args.cold:
+        flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+        red = torch.empty((), dtype=torch.int32, device=dev)
     for _ in range(args.iters):
+        if args.cold:
+            flush.zero_()
+            torch.amax(flush, dim=0, out=red)
         call()
     torch.cuda.synchronize()
     print(f"prof_workload {cfg.name}: {args.iters} launches done", flush=True)
