@@ -286,9 +286,14 @@ def main():
                      "achieved": round(achieved, 2), "peak": MI355X_BF16_DENSE_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / MI355X_BF16_DENSE_TFLOPS, 4),
                      "traffic": traffic.get("hbm_bytes_per_launch"),
+                     "frac_at_median": round(value / MI355X_BF16_DENSE_TFLOPS, 4),
                      "avg_launch_us": round(mean_ms * 1e3, 2),
-                     "avg_launch_timing": "mean of the cold steps' event times (each event pair "
-                                          "also holds the launch's dispatch, a few µs)",
+                     "avg_launch_timing": "achieved and frac: the mean of the cold steps' event "
+                                          "times (each event pair also holds the launch's "
+                                          "dispatch, a few µs, so the kernel alone runs faster: "
+                                          "rocprof_cold_kernel_us is the mean kernel time of the "
+                                          "cold steps in the committed rocprofv3 trace of this "
+                                          "same command); frac_at_median: at the median event time",
                      "rocprof_cold_kernel_us": trace_cold_mean(),
                      "algorithmic_flop_per_launch": cfg.flops,
                      "algorithmic_bytes_per_launch": cfg.algorithmic_bytes,
