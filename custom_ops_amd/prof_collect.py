@@ -63,12 +63,13 @@ STALL_PASSES = {
 
 
 COLD = False   # --cold: every counted launch after a cache flush
+VARIANT = ""   # --variant: kernel-variant fields passed to every call
 
 
 def workload_cmd(cfg: str, iters: int, bcast: bool = False) -> list[str]:
     return [sys.executable, "-m", "custom_ops_amd.prof_workload", "--config", cfg, "--iters",
             str(iters), "--copy-mib", str(COPY_MIB), *(["--mask-bcast"] if bcast else []),
-            *(["--cold"] if COLD else [])]
+            *(["--cold"] if COLD else []), *(["--variant", VARIANT] if VARIANT else [])]
 
 
 def rocprof_cmd(name: str, outdir: str, cfg: str, iters: int) -> list[str]:
@@ -275,13 +276,16 @@ def main() -> None:
     ap.add_argument("--stall", action="store_true", help="wave-state counters instead")
     ap.add_argument("--cold", action="store_true",
                     help="flush the caches before every counted launch (the bench's cold launches)")
+    ap.add_argument("--variant", default="",
+                    help="kernel-variant fields for every call, e.g. order=1 (summaries get a suffix)")
     ap.add_argument("--bench", action="store_true", help="kernel trace of bench.py's timed run instead")
     ap.add_argument("--power", action="store_true", help="socket power and clocks per workload instead")
     ap.add_argument("--loop-s", type=float, default=10.0, help="--power: seconds per workload")
     args = ap.parse_args()
     args.out = os.path.abspath(args.out)      # the passes run with cwd=/tmp
-    global COLD
+    global COLD, VARIANT
     COLD = args.cold
+    VARIANT = args.variant
     os.makedirs(args.out, exist_ok=True)
     sys.path.insert(0, ROOT)
     from custom_ops_amd.workloads import CONFIGS
@@ -336,7 +340,8 @@ def main() -> None:
     bank_conf = ld["SQ_LDS_BANK_CONFLICT"] / max(1.0, ld["SQ_LDS_IDX_ACTIVE"])
 
     kname = attn[0]["Name"]
-    stem = f"fa_fwd_kernel_{cfg.name}" + ("_cold" if COLD else "")
+    stem = (f"fa_fwd_kernel_{cfg.name}" + ("_cold" if COLD else "")
+            + ("_" + VARIANT.replace("=", "").replace(",", "_") if VARIANT else ""))
     # The counted launches are the last --iters of each kernel in the trace
     # (the clock-settle launches come first): their mean duration, and for
     # a launch sequence the mean of (end of its last kernel - start of the
@@ -426,7 +431,7 @@ def main() -> None:
     lines.append("")
     lines.append("commands (run from the repository root; each pass is its own process):")
     lines.append(f"  python -m custom_ops_amd.prof_collect --config {cfg.name} --iters {args.iters}"
-                 + (" --cold" if COLD else ""))
+                 + (" --cold" if COLD else "") + (f" --variant {VARIANT}" if VARIANT else ""))
     for p in PASSES:
         lines.append("  cd /tmp && TMPDIR=/tmp PYTHONPATH=<repo> " +
                      " ".join(rocprof_cmd(p, f"<out>/raw/{p}", cfg.name, args.iters)))

@@ -3,7 +3,7 @@ configuration, optionally preceded by a plain device copy of known size (the
 calibration kernel for the FETCH_SIZE / WRITE_SIZE counters).
 
     python -m custom_ops_amd.prof_workload --config cfg2 --iters 20 [--copy-mib 512]
-        [--mask-bcast]
+        [--mask-bcast] [--cold] [--variant order=1]
     python -m custom_ops_amd.prof_workload --config cfg2 --loop-s 10
 
 --mask-bcast launches the same call through the C ABI with the mask's row and
@@ -38,6 +38,8 @@ def main() -> None:
                     help="mask row/batch strides 0: one L2-resident mask row for every query row")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run 5 copies of a buffer of this many MiB (read N, write N)")
+    ap.add_argument("--variant", default="",
+                    help="kernel-variant fields for every call, e.g. order=1,waves=8 (custom_ops_amd.Variant)")
     ap.add_argument("--cold", action="store_true",
                     help="flush the caches (512 MiB zero + read-back) before every counted launch")
     ap.add_argument("--loop-s", type=float, default=0.0,
@@ -61,10 +63,15 @@ def main() -> None:
     cfg = CONFIGS[args.config]
     q, k, v, m = (t.to(dev) for t in make_inputs(cfg))
     call = lambda: ops.mha_fwd_with_mask(q, k, v, m)  # noqa: E731
+    var = None
+    if args.variant:
+        from custom_ops_amd import Variant, mha_fwd_with_mask
+        var = Variant(**{kv.split("=")[0]: int(kv.split("=")[1]) for kv in args.variant.split(",")})
+        call = lambda: mha_fwd_with_mask(q, k, v, m, variant=var)  # noqa: E731
     if args.mask_bcast:
         from custom_ops_amd import _lib, fa
         out = torch.empty_like(q)
-        p = fa.make_params(q, k, v, m, out)
+        p = fa.make_params(q, k, v, m, out, 0, var)
         p.mask_row_stride = 0
         p.mask_batch_stride = 0
         ws_bytes = _lib.workspace_bytes(p)
