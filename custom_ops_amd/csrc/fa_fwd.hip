@@ -516,8 +516,10 @@ __device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int row
 // would each read its dead mask once more. A lane reads 16 bytes = 8 entries
 // of one row (8 lanes per tile row, the chunks of the scan, unaligned loads
 // cost no more here than aligned ones): a chunk below Sk is live unless its
-// four words are all the -inf pair, and only the chunk that holds Sk checks
-// entry by entry. Every map byte is written by exactly one workgroup, so the
+// four words are all the -inf pair, and only the chunk that holds Sk is
+// checked entry by entry, read shifted back to end at column Sk - 1 (a
+// 16-byte load reaching past the buffer's end would read its in-range
+// entries as 0, i.e. visible). Every map byte is written by exactly one workgroup, so the
 // map needs no clearing.
 template <bool BF16>
 __global__ __launch_bounds__(256) void live_map_kernel(KParams p) {
@@ -542,9 +544,13 @@ __global__ __launch_bounds__(256) void live_map_kernel(KParams p) {
       const int c = base + u * kThreads + (int)threadIdx.x;
       const int c0 = c_lo + 8 * (c & (kChunksPerRow - 1));
       const bool in = c < total && c0 < c_hi;
+      // the chunk that holds Sk is read shifted back to end at column Sk - 1:
+      // a 16-byte load that reaches past the buffer's end reads 0 for its
+      // in-range entries too (and 0 is visible)
+      const int sh = max(c0 + 8 - c_hi, 0);
+      const uint32_t off = ((uint32_t)(m0 + (c >> 6)) * (uint32_t)p.m_rs + (uint32_t)(c0 - sh)) * 2u;
       // outside: an out-of-range offset, which reads 0 without an access
-      v[u] = bload16(rm, in ? ((uint32_t)(m0 + (c >> 6)) * (uint32_t)p.m_rs + (uint32_t)c0) * 2u
-                            : 0xfffffff0u);
+      v[u] = bload16(rm, in ? off : 0xfffffff0u);
     }
     uint32_t mine = 0u;
 #pragma unroll
@@ -554,7 +560,16 @@ __global__ __launch_bounds__(256) void live_map_kernel(KParams p) {
       if (c >= total || c0 >= c_hi) continue;
       bool live = !((v[u][0] == kNegPair) & (v[u][1] == kNegPair) & (v[u][2] == kNegPair) &
                     (v[u][3] == kNegPair));
-      if (c0 + 8 > c_hi) live = live8<BF16>(v[u], c0, c_hi);   // the chunk that holds Sk
+      if (c0 + 8 > c_hi) {   // the chunk that holds Sk: its entries sh .. 7 are columns c0 .. Sk - 1
+        const int sh = c0 + 8 - c_hi;
+        constexpr uint32_t kNeg = kNegPair & 0xffffu;
+        live = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          live |= (2 * i >= sh) & ((v[u][i] & 0xffffu) != kNeg);
+          live |= (2 * i + 1 >= sh) & ((v[u][i] >> 16) != kNeg);
+        }
+      }
       if (live) mine |= 1u << ((c & (kChunksPerRow - 1)) >> 3);
     }
     // once every tile of the group is known live (a dense mask: after the

@@ -122,3 +122,61 @@ def test_live_range_parity(gpu, loop):
         if splits == 1:
             assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), \
                 f"loop {loop} case {n} {kind}: narrowed unsplit launch differs"
+
+
+MAP_CASES = [  # kind, b, h, hk, sq, sk, d, dtype, splits, extra mask cols, extra mask rows, waves
+    ("causal", 2, 16, 4, 1000, 4099, 128, torch.bfloat16, 2, 0, 0, 8),    # last tile dead in every row block
+    ("causal", 1, 4, 1, 1000, 3001, 128, torch.bfloat16, 1, 0, 0, 4),
+    ("window", 2, 16, 4, 1000, 4099, 128, torch.bfloat16, 2, 0, 0, 8),
+    ("window", 2, 4, 2, 301, 777, 128, torch.bfloat16, 1, 0, 0, 8),
+    ("pad", 1, 4, 1, 300, 3001, 128, torch.bfloat16, 5, 0, 0, 4),
+    ("trap_cols", 1, 2, 2, 256, 1030, 128, torch.bfloat16, 1, 3, 0, 8),
+    ("rows_past_sq", 1, 2, 2, 200, 1021, 128, torch.float16, 2, 0, 56, 4),
+    ("last_tile", 2, 4, 1, 130, 3001, 64, torch.bfloat16, 1, 0, 0, 4),
+]
+
+
+@pytest.mark.gpu
+def test_live_map_matches_host(gpu):
+    """The live-tile map itself, read back from the workspace (its last
+    region: ``[B][m-blocks][ceil(tiles / 8)]`` bytes rounded up to 256),
+    against the tiles that hold a visible entry of a row < Sq in a column < Sk,
+    recomputed on the host. Covers the chunk that holds Sk in the last row of
+    the mask, whose 16-byte load would reach past the buffer's end."""
+    import ctypes
+    from custom_ops_amd import _lib, Variant
+    from custom_ops_amd.fa import make_params
+    lib = _lib.load()
+    for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr, waves) in enumerate(MAP_CASES):
+        g = torch.Generator().manual_seed(2000 + n)
+        q = torch.randn(b, h, sq, d, generator=g).to(dt).cuda()
+        k = torch.randn(b, hk, sk, d, generator=g).to(dt).cuda()
+        m = mask_of(kind, b, sq, sk, sk + xc, sq + xr, g).to(dt).cuda()
+        assert (sk + xc) % 8 != 0
+        out = torch.empty_like(q)
+        var = Variant(waves=waves, live=1)
+        p = make_params(q, k, k, m, out, splits, var)
+        nbytes = lib.mi355_fa_workspace_bytes(ctypes.byref(p))
+        ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
+        p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+        err = ctypes.create_string_buffer(512)
+        rc = lib.mi355_fa_fwd(ctypes.byref(p), torch.cuda.current_stream().cuda_stream, err, 512)
+        assert rc == 0, err.value
+        torch.cuda.synchronize()
+        pack = 1
+        while pack * 2 <= 4 and (h // hk) % (pack * 2) == 0:
+            pack *= 2
+        rows = 32 * waves // pack
+        num_m, nn = -(-sq // rows), -(-sk // 64)
+        row_bytes = -(-nn // 8)
+        size = b * num_m * row_bytes
+        off = nbytes - ((size + 255) & ~255)
+        mp = ws[off: off + size].cpu().view(b, num_m, row_bytes)
+        vis = ~torch.isinf(m[:, 0, :sq, :sk].float().cpu())
+        for bb in range(b):
+            for rb in range(num_m):
+                rr = vis[bb, rb * rows: min(sq, (rb + 1) * rows)]
+                for t in range(nn):
+                    want = bool(rr[:, t * 64:(t + 1) * 64].any())
+                    got = bool((int(mp[bb, rb, t // 8]) >> (t % 8)) & 1)
+                    assert want == got, f"case {n} {kind}: batch {bb} row block {rb} tile {t}: map {got}"
