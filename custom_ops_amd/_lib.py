@@ -34,7 +34,7 @@ EXPORTED = (
     "mi355_fa_abi_version",
     "mi355_fa_build_info",
 )
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class Variant(ctypes.Structure):
@@ -44,7 +44,7 @@ class Variant(ctypes.Structure):
 
     _fields_ = [(name, ctypes.c_int32) for name in
                 ("waves", "pack", "order", "loop", "fuse", "live", "deep", "mask_mfma", "stream",
-                 "live_map")]
+                 "live_map", "stage")]
 
     def __repr__(self) -> str:
         set_ = {n: getattr(self, n) for n, _ in self._fields_ if getattr(self, n)}

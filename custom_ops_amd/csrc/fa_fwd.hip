@@ -205,14 +205,21 @@ struct KParams {
   // K/V tiles are read by exactly one workgroup each: the compiled kernel
   // streams them with the non-temporal hint
   int kv_nt;
-  // Live-tile map written by live_map_kernel before this launch (or null):
-  // bit t of byte (b·num_m + m-block)·map_row_bytes + t/8 is set when tile t
-  // holds a visible entry of the m-block's rows. With it the workgroups read
-  // their live ranges instead of scanning the mask.
+  // Live-tile map written by mask_stage_kernel before this launch (or null):
+  // bit t % 8 of byte (b·map_slices + r / 16)·map_row_bytes + t / 8 is set
+  // when tile t holds a visible entry of row r (rows in slices of 16). With it
+  // the workgroups read their live ranges instead of scanning the mask.
   const uint8_t* live_map;
-  int map_row_bytes;
-  int map_rows;              // rows per m-block (BM / pack)
-  uint8_t* live_map_out;     // the same map, for live_map_kernel
+  int map_row_bytes;         // bytes per slice: ceil(num_n / 8)
+  int map_slices;            // slices per batch: ceil(Sq / 16)
+  uint8_t* live_map_out;     // the same map, for mask_stage_kernel
+  // The mask as the caller passed it, for mask_stage_kernel: with a staged
+  // copy, mask / m_bs / m_rs / msq above describe the copy instead
+  const uint16_t* msrc;
+  int64_t msrc_bs;
+  int msrc_rs, msrc_q;
+  uint16_t* stage_out;       // the staged copy [B][Sq][stage_rs] (or null)
+  int stage_rs;              // ceil(Sk / 8) · 8
 };
 
 // Workgroup-id remap: the hardware hands linear id L to XCD (L % 8). Give each
@@ -435,6 +442,24 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t x) {
          __builtin_amdgcn_readlane(x, 32) | __builtin_amdgcn_readlane(x, 48);
 }
 
+// min and max over the wave, the same pattern as wave_or (a uniform result)
+__device__ __forceinline__ int wave_min(int x) {
+  x = min(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+  x = min(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+  x = min(x, __builtin_amdgcn_mov_dpp(x, 0x124, 0xF, 0xF, false));
+  x = min(x, __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false));
+  return min(min(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             min(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+__device__ __forceinline__ int wave_max(int x) {
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x124, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false));
+  return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
 // OR over the workgroup: wave_or, then one word per wave in LDS (set `set` of
 // two), read by every thread after a barrier
 template <int NT>
@@ -477,24 +502,41 @@ __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams
 }
 
 // The live range of the workgroup's row block from the live-tile map: the
-// first and the last set bit of its row of the map (the same [lo, hi] the
-// scan below finds, so the same split ranges and the same results).
+// first and the last set bit over the map slices of its rows (the same
+// [lo, hi] the scan below finds, so the same split ranges and the same
+// results).
 template <int NT>
 __device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int rows, uint32_t* red) {
+  constexpr int kW = NT / 64;
   const int tid = threadIdx.x;
   const int nbytes = uni(p.map_row_bytes);
-  const uint8_t* row = p.live_map + ((int64_t)ti.b * p.num_m + ti.m0 / rows) * nbytes;
-  if (tid == 0) { red[0] = 0x7fffffffu; red[1] = 0u; }
-  __syncthreads();
-  for (int i = tid; i < nbytes; i += NT) {
-    const uint32_t v = row[i];
+  const int s0 = ti.m0 >> 4, s1 = min((ti.m0 + rows + 15) >> 4, p.map_slices);
+  const uint8_t* map = p.live_map + ((int64_t)ti.b * p.map_slices + s0) * nbytes;
+  int mlo = 0x7fffffff, mhi = 0;
+  for (int i = tid; i < (s1 - s0) * nbytes; i += NT) {
+    const uint32_t v = map[i];
     if (v) {
-      atomicMin(reinterpret_cast<int*>(red), i * 8 + __builtin_ctz(v));
-      atomicMax(reinterpret_cast<int*>(red + 1), i * 8 + 32 - __builtin_clz(v));   // one past the last
+      const int t0 = (i % nbytes) * 8;
+      mlo = min(mlo, t0 + __builtin_ctz(v));
+      mhi = max(mhi, t0 + 32 - __builtin_clz(v));   // one past the last
     }
   }
+  // per wave by DPP, then one slot per wave (no LDS atomics: the compiler's
+  // whole-wave reduction for them needs registers the assembly loops lack)
+  mlo = wave_min(mlo);
+  mhi = wave_max(mhi);
+  int* w = reinterpret_cast<int*>(red);
+  if ((tid & 63) == 0) {
+    w[2 * (tid >> 6)] = mlo;
+    w[2 * (tid >> 6) + 1] = mhi;
+  }
   __syncthreads();
-  int lo = (int)__builtin_amdgcn_readfirstlane(red[0]), hi = (int)__builtin_amdgcn_readfirstlane(red[1]) - 1;
+#pragma unroll
+  for (int i = 0; i < kW; ++i) {
+    mlo = min(mlo, w[2 * i]);
+    mhi = max(mhi, w[2 * i + 1]);
+  }
+  int lo = (int)__builtin_amdgcn_readfirstlane(mlo), hi = (int)__builtin_amdgcn_readfirstlane(mhi) - 1;
   __syncthreads();                         // every wave has read `red` before any DMA lands
   if (lo > hi) { lo = 0; hi = -1; }        // no visible entry in these rows
   if (lo == 0 && hi == p.num_n - 1) return false;   // whole axis live: the nominal ranges stand
@@ -506,82 +548,106 @@ __device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int row
   return true;
 }
 
-// Live-tile map of a launch whose mask rows are not 16-byte aligned (a mask
-// of Sk % 8 != 0 columns): one workgroup per (batch, m-block, 8 KV tiles)
-// writes the map byte of those tiles, bit t set when tile t has an entry that
-// is not -inf in a column < Sk of a row < Sq of the m-block. The launch's
-// workgroups then read their live ranges from the map (range_from_map)
-// instead of each scanning its rows' mask: the rows of an m-block are shared
-// by every head group and split of it (8 workgroups on cfg5's shape), which
-// would each read its dead mask once more. A lane reads 16 bytes = 8 entries
-// of one row (8 lanes per tile row, the chunks of the scan, unaligned loads
-// cost no more here than aligned ones): a chunk below Sk is live unless its
-// four words are all the -inf pair, and only the chunk that holds Sk is
-// checked entry by entry, read shifted back to end at column Sk - 1 (a
-// 16-byte load reaching past the buffer's end would read its in-range
-// entries as 0, i.e. visible). Every map byte is written by exactly one workgroup, so the
-// map needs no clearing.
+// Pre-pass for a mask whose rows are not 16-byte aligned (a mask of
+// Sk % 8 != 0 columns, or one that starts off a 16-byte boundary): one
+// workgroup per (batch, 16 rows, 8 KV tiles) reads those rows' 512 columns
+// once (rows < Sq, columns < Sk) and
+//  * with stage_out, writes them to the staged copy [B][Sq][stage_rs], whose
+//    rows are 16-byte aligned, the columns Sk .. stage_rs - 1 -inf: the
+//    attention kernel then takes its mask tiles by LDS DMA, as from an
+//    aligned mask (the reference pads the mask for Sk % 8 != 0 as well,
+//    csrc/fa/fa_fwd_op.cu:117-134);
+//  * with live_map_out, writes one map byte, bit t set when tile t of the
+//    group has an entry that is not -inf: the launch's workgroups then read
+//    their live ranges from the map (range_from_map) instead of each scanning
+//    its rows' mask, which the 8 workgroups sharing an m-block on cfg5's shape
+//    would each read again.
+// Each wave takes one row's 512 columns per step and reads them as aligned
+// 16-byte blocks from the 16-byte boundary at or below their start (lane i
+// block i, lane 63 also block 64); lane i's 8 entries are the end of its
+// block and the start of the next lane's (ds_bpermute), aligned by the row's
+// byte offset, which is the same for the whole wave. Unaligned 16-byte loads
+// ran at half the rate (8.4 MB: 6.5 against 3.7 µs for the map alone). The
+// descriptor covers whole 16-byte blocks, from the block that holds the
+// batch's first entry to the one that holds its last: those lie in the pages
+// of the mask's own bytes, and no load reaches past the descriptor (a load
+// that does reads 0 for its in-range bytes too, and 0 is visible). Entries of
+// columns >= Sk and rows >= Sq are not counted and are staged as -inf. Every
+// map byte and every staged chunk has one writer, so neither needs clearing.
 template <bool BF16>
-__global__ __launch_bounds__(256) void live_map_kernel(KParams p) {
+__global__ __launch_bounds__(256) void mask_stage_kernel(KParams p) {
   constexpr uint32_t kNegPair = BF16 ? 0xff80ff80u : 0xfc00fc00u;
-  constexpr int kThreads = 256, kBatch = 4, kChunksPerRow = 8 * 8;   // 8 tiles x 8 chunks
+  constexpr uint32_t kNeg = kNegPair & 0xffffu;
+  constexpr int kThreads = 256, kRows = 16, kChunksPerRow = 8 * 8;   // 8 tiles x 8 chunks
+  constexpr int kSteps = kRows * kChunksPerRow / kThreads;          // rows per wave
   const int g = blockIdx.x % p.map_row_bytes;          // 8-tile group
-  const int rb = (blockIdx.x / p.map_row_bytes) % p.num_m;
-  const int b = blockIdx.x / (p.map_row_bytes * p.num_m);
-  const int m0 = rb * p.map_rows;
-  const int nr = min(p.map_rows, p.sq - m0);
-  const rsrc_t rm = make_rsrc(p.mask + (int64_t)b * p.m_bs, (uint32_t)p.msq * p.m_rs * 2u);
-  const int c_lo = g * 8 * kBN, c_hi = min(c_lo + 8 * kBN, p.sk);   // columns of this group, < Sk
-  const uint32_t full = (1u << ((c_hi - c_lo + kBN - 1) / kBN)) - 1u;   // every tile of the group live
+  const int sl = (blockIdx.x / p.map_row_bytes) % p.map_slices;
+  const int b = blockIdx.x / (p.map_row_bytes * p.map_slices);
+  const int r0 = sl * kRows;
+  const int nr = min(kRows, p.sq - r0);
+  const uintptr_t bsrc = reinterpret_cast<uintptr_t>(p.msrc + (int64_t)b * p.msrc_bs);
+  const uintptr_t abase = bsrc & ~(uintptr_t)15;
+  const uint32_t lead = (uint32_t)(bsrc - abase);
+  const uint32_t nrec = (lead + (uint32_t)p.msrc_q * (uint32_t)p.msrc_rs * 2u + 15u) & ~15u;
+  const rsrc_t rm = make_rsrc(reinterpret_cast<const void*>(abase), nrec);
+  const int sk = p.sk;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  u32x4 v[kSteps], x[kSteps];
+  uint32_t dl[kSteps];
+#pragma unroll
+  for (int u = 0; u < kSteps; ++u) {
+    const int row = u * (kThreads / 64) + wave;       // wave-uniform
+    const uint32_t seg = lead + ((uint32_t)(r0 + row) * (uint32_t)p.msrc_rs + (uint32_t)(g * 8 * kBN)) * 2u;
+    const uint32_t a = seg & ~15u;
+    dl[u] = seg - a;                                  // 0 .. 14, even
+    const bool in = row < nr;
+    // outside: an out-of-range offset, which reads 0 without an access
+    v[u] = bload16(rm, in ? a + 16u * (uint32_t)lane : 0xfffffff0u);
+    x[u] = bload16(rm, (in && lane == 63) ? a + 1024u : 0xfffffff0u);
+  }
+  uint32_t mine = 0u;
+#pragma unroll
+  for (int u = 0; u < kSteps; ++u) {
+    const int row = u * (kThreads / 64) + wave;
+    const int c0 = g * 8 * kBN + 8 * lane;
+    u32x4 nx;   // the next lane's block (lane 63: its own second load)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane + 1) & 63) * 4, (int)v[u][i]);
+      nx[i] = lane == 63 ? x[u][i] : t;
+    }
+    const uint32_t cat[8] = {v[u][0], v[u][1], v[u][2], v[u][3], nx[0], nx[1], nx[2], nx[3]};
+    const uint32_t q = dl[u] >> 2, sh = dl[u] & 3u;   // whole words, then bytes
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t lo = cat[j], hi = cat[j + 1];
+#pragma unroll
+      for (int k = 1; k < 4; ++k)
+        if (q == (uint32_t)k) { lo = cat[j + k]; hi = cat[j + k + 1]; }
+      w[j] = __builtin_amdgcn_alignbyte(hi, lo, sh);
+    }
+    if (row >= nr || c0 >= sk) continue;
+    if (c0 + 8 > sk) {   // the chunk that holds Sk: -inf from column Sk on
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (c0 + j >= sk)
+          w[j >> 1] = (j & 1) ? ((w[j >> 1] & 0xffffu) | (kNeg << 16)) : ((w[j >> 1] & 0xffff0000u) | kNeg);
+    }
+    const bool live = !((w[0] == kNegPair) & (w[1] == kNegPair) & (w[2] == kNegPair) & (w[3] == kNegPair));
+    if (live) mine |= 1u << (lane >> 3);
+    if (p.stage_out)
+      *reinterpret_cast<u32x4*>(p.stage_out + ((int64_t)b * p.sq + r0 + row) * p.stage_rs + c0) = w;
+  }
+  if (!p.live_map_out) return;
   __shared__ uint32_t bits;
   if (threadIdx.x == 0) bits = 0u;
   __syncthreads();
-  const int total = nr * kChunksPerRow;
-  for (int base = 0; base < total; base += kThreads * kBatch) {
-    u32x4 v[kBatch];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int c = base + u * kThreads + (int)threadIdx.x;
-      const int c0 = c_lo + 8 * (c & (kChunksPerRow - 1));
-      const bool in = c < total && c0 < c_hi;
-      // the chunk that holds Sk is read shifted back to end at column Sk - 1:
-      // a 16-byte load that reaches past the buffer's end reads 0 for its
-      // in-range entries too (and 0 is visible)
-      const int sh = max(c0 + 8 - c_hi, 0);
-      const uint32_t off = ((uint32_t)(m0 + (c >> 6)) * (uint32_t)p.m_rs + (uint32_t)(c0 - sh)) * 2u;
-      // outside: an out-of-range offset, which reads 0 without an access
-      v[u] = bload16(rm, in ? off : 0xfffffff0u);
-    }
-    uint32_t mine = 0u;
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int c = base + u * kThreads + (int)threadIdx.x;
-      const int c0 = c_lo + 8 * (c & (kChunksPerRow - 1));
-      if (c >= total || c0 >= c_hi) continue;
-      bool live = !((v[u][0] == kNegPair) & (v[u][1] == kNegPair) & (v[u][2] == kNegPair) &
-                    (v[u][3] == kNegPair));
-      if (c0 + 8 > c_hi) {   // the chunk that holds Sk: its entries sh .. 7 are columns c0 .. Sk - 1
-        const int sh = c0 + 8 - c_hi;
-        constexpr uint32_t kNeg = kNegPair & 0xffffu;
-        live = false;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          live |= (2 * i >= sh) & ((v[u][i] & 0xffffu) != kNeg);
-          live |= (2 * i + 1 >= sh) & ((v[u][i] >> 16) != kNeg);
-        }
-      }
-      if (live) mine |= 1u << ((c & (kChunksPerRow - 1)) >> 3);
-    }
-    // once every tile of the group is known live (a dense mask: after the
-    // first batch) the rest need not be read
-    mine = wave_or(mine);   // one LDS atomic per wave, not per thread
-    if ((threadIdx.x & 63) == 0 && mine) atomicOr(&bits, mine);
-    __syncthreads();
-    if (bits == full) break;
-    __syncthreads();        // every wave has read `bits` before the next batch's atomics
-  }
+  mine = wave_or(mine);   // one LDS atomic per wave, not per thread
+  if ((threadIdx.x & 63) == 0 && mine) atomicOr(&bits, mine);
+  __syncthreads();
   if (threadIdx.x == 0)
-    p.live_map_out[((int64_t)b * p.num_m + rb) * p.map_row_bytes + g] = (uint8_t)bits;
+    p.live_map_out[((int64_t)b * p.map_slices + sl) * p.map_row_bytes + g] = (uint8_t)bits;
 }
 
 template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool MAP = false>
@@ -1390,9 +1456,13 @@ void fa_fwd_kernel(const KParams p) {
   static_assert(kTailOwn || !SPLIT || kTailFloats * 4 <= NSS * G::kVElems * 2, "tail fits in the V stages");
   __shared__ __align__(16) float sTail[kTailOwn ? kTailFloats : 1];
 
+  // Live ranges from the live-tile map: every kernel but the 4-wave deep ones
+  // on the LDS-DMA mask path, whose SGPRs it would push into spills (they
+  // scan)
+  constexpr bool kMap = !MDIRECT || WAVES == 8 || !DEEP;
   TileIdx ti = tile_index<G::kBM>(p);
   const TileIdx tg = ti;   // the workgroup's first head and row
-  const LiveProbe lp = live_probe<G::kThreads, !MDIRECT>(tg, p);
+  const LiveProbe lp = live_probe<G::kThreads, kMap>(tg, p);
   place_wave(ti, p, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), 32);
   A a(p);
   a.init(ti);
@@ -1427,7 +1497,7 @@ void fa_fwd_kernel(const KParams p) {
   {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
-    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, !MDIRECT>(tn, p, G::kBM / p.pack, lp,
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, kMap>(tn, p, G::kBM / p.pack, lp,
                                                        reinterpret_cast<uint32_t*>(KS(NST - 1)))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
@@ -2073,8 +2143,11 @@ struct Plan {
   int mask_mfma_off;   // the compiled kernel widens bf16 masks on the VALU
   int kv_nt;           // every K/V tile is read by one workgroup: non-temporal loads
   int live_map;        // a live-tile map pre-pass serves the live ranges (unaligned mask rows)
-  int map_row_bytes;
+  int map_row_bytes, map_slices;
   size_t map_bytes;
+  int staged;          // unaligned mask rows copied to an aligned staged mask
+  int stage_rs;
+  size_t stage_bytes;
 };
 
 // Tile plan: the workgroup size (4 or 8 waves) and split count with the
@@ -2146,7 +2219,7 @@ static int order_head_major(const mi355_fa_params* p, const Plan& pl, int cus,
   return 0;
 }
 
-static Plan make_plan(const mi355_fa_params* p, int cus) {
+static Plan make_plan(const mi355_fa_params* p, int cus, bool allow_stage = true) {
   Plan pl{};
   const mi355_fa_variant v = variant_of(p);
   pl.pack = pick_pack(p, v);
@@ -2197,17 +2270,32 @@ static Plan make_plan(const mi355_fa_params* p, int cus) {
   }
   pl.loop = v.loop < 0 ? 0 : (v.loop >= 1 && v.loop <= 3 ? v.loop : 3);
   pl.live = v.live < 0 ? 0 : (v.live > 0 ? 1 : 2);
-  // Masks whose rows are not 16-byte aligned run the compiled kernel, which
-  // narrows every launch (live on); their live ranges come from a pre-pass
-  // map instead of each workgroup's scan.
+  // A mask whose rows are not 16-byte aligned goes through a pre-pass that
+  // copies it to an aligned staged mask in the workspace (rows < Sq, columns
+  // padded with -inf to a multiple of 8), so that every kernel takes its mask
+  // tiles by LDS DMA, and writes the live-tile map that serves the live
+  // ranges in place of each workgroup's scan. Variant stage = -1 (and callers
+  // without room for the copy) keep the mask in place: the compiled kernel
+  // then reads it through registers, with the map.
   {
     const bool mask_direct = ((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
                              (p->mask_row_stride & 7) == 0;
     pl.live_map = !mask_direct && pl.live != 0 && pl.num_n >= 4 && v.live_map >= 0;
     pl.map_row_bytes = ceil_div(pl.num_n, 8);
-    pl.map_bytes = pl.live_map ? (((size_t)p->b * pl.num_m * pl.map_row_bytes + 255) & ~(size_t)255) : 0;
+    pl.map_slices = ceil_div(p->seqlen_q, 16);
+    pl.map_bytes = pl.live_map ? (((size_t)p->b * pl.map_slices * pl.map_row_bytes + 255) & ~(size_t)255) : 0;
+    pl.stage_rs = ceil_div(p->seqlen_k, 8) * 8;
+    // Staged by default except for 8-wave split launches, which run the
+    // compiled kernel either way: there the copy's writes cost what the LDS
+    // DMA saves (cfg5 44.9 staged against 44.7 µs in place, same session),
+    // while unsplit launches reach the assembly loops ([4,16,16,2048,2047]
+    // random mask 150 against 178 µs, top-left causal 139 against 157).
+    pl.staged = !mask_direct && allow_stage && v.stage >= 0 && p->seqlen_k >= 8 &&
+                (uint64_t)p->seqlen_q * pl.stage_rs * 2 < (1ull << 31) &&
+                (v.stage > 0 || !(pl.splits > 1 && pl.waves == 8));
+    pl.stage_bytes = pl.staged ? (((size_t)p->b * p->seqlen_q * pl.stage_rs * 2 + 255) & ~(size_t)255) : 0;
   }
-  pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes + pl.map_bytes;
+  pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes + pl.map_bytes + pl.stage_bytes;
   // A 4-wave grid that puts at most one workgroup on each CU takes a third K/V
   // stage (112 KiB of LDS at d = 128: one workgroup per CU; cfg4 cold -7 %).
   {
@@ -2313,7 +2401,11 @@ template <int D, bool BF16>
 static bool runs_asm_loop(const KParams& kp, const Plan& pl) {
   // bf16 adds the mask on the matrix core, which needs bf16(1/scale) > 1.0078
   // (-max_bf16 · (1/scale) must overflow to -inf): scale < 0.99
-  return D == 128 && pl.waves == 8 && kp.mask_direct && pl.loop && (!BF16 || kp.scale < 0.99f);
+  // A staged mask's split launches run the compiled kernel, which reads the
+  // live ranges from the map (the loops would scan the staged copy per
+  // workgroup: cfg5's window 57.8 µs against 44.2 hot).
+  return D == 128 && pl.waves == 8 && kp.mask_direct && pl.loop && (!BF16 || kp.scale < 0.99f) &&
+         !(pl.staged && pl.live_map && pl.splits > 1);
 }
 
 template <int D, bool BF16, bool SPLIT>
@@ -2338,13 +2430,16 @@ static hipError_t launch(const KParams& kp_in, const CParams& cp, const Plan& pl
   KParams kp = kp_in;
   const int lm = pl.live;
   kp.live = pl.num_n >= 4 && (lm == 1 || (lm == 2 && (pl.splits > 1 || !runs_asm_loop<D, BF16>(kp, pl))));
-  if (kp.live && kp.live_map_out) {
-    hipLaunchKernelGGL((live_map_kernel<BF16>), dim3((unsigned)(kp.b * kp.num_m * kp.map_row_bytes)), dim3(256), 0,
-                       st, kp);
+  const bool want_map = kp.live && kp.live_map_out;
+  if (kp.stage_out || want_map) {
+    KParams km = kp;
+    if (!want_map) km.live_map_out = nullptr;
+    hipLaunchKernelGGL((mask_stage_kernel<BF16>), dim3((unsigned)(kp.b * kp.map_slices * kp.map_row_bytes)),
+                       dim3(256), 0, st, km);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    kp.live_map = kp.live_map_out;
   }
+  kp.live_map = want_map ? kp.live_map_out : nullptr;
   if (pl.splits == 1) return launch_variant<D, BF16, false>(kp, pl, st);
   // the fused tail is in the compiled kernel only (the assembly loops keep no
   // registers for it): their split launches keep the combine launch
@@ -2391,7 +2486,11 @@ size_t mi355_fa_workspace_bytes(const mi355_fa_params* p) {
   return make_plan(p, device_info().cus).ws_bytes;
 }
 
-int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errlen) {
+}  // extern "C"
+
+// The launch behind both entry points; allow_stage false plans without the
+// staged mask (mi355_fa_fwd_noalloc when the copy would not fit its scratch).
+static int fwd_impl(const mi355_fa_params* p, void* stream, char* err, size_t errlen, bool allow_stage) {
   int rc = validate(p, err, errlen);
   if (rc) return rc;
   if (p->b == 0 || p->h == 0 || p->seqlen_q == 0) return MI355_FA_OK;
@@ -2400,7 +2499,7 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
     set_err(err, errlen, "mi355_fa: current HIP device is not gfx950 (MI355X)");
     return MI355_FA_EDEVICE;
   }
-  const Plan pl = make_plan(p, dev.cus);
+  const Plan pl = make_plan(p, dev.cus, allow_stage);
   const int64_t total = (int64_t)p->b * (p->h / pl.pack) * pl.num_m * pl.splits;
   if (total >= (1LL << 24)) {
     set_err(err, errlen, "problem too large: %lld workgroups", (long long)total);
@@ -2426,7 +2525,8 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   const bool split = pl.splits > 1;
   if (pl.ws_bytes && (!p->workspace || p->workspace_bytes < pl.ws_bytes)) {
     set_err(err, errlen, "%s needs %zu workspace bytes, got %zu",
-            split ? "split-KV" : "the live-tile map", pl.ws_bytes, p->workspace_bytes);
+            split ? "split-KV" : (pl.staged ? "the staged mask" : "the live-tile map"), pl.ws_bytes,
+            p->workspace_bytes);
     return MI355_FA_EWORKSPACE;
   }
 
@@ -2458,11 +2558,22 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   kp.mask_direct = (((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
                     (p->mask_row_stride & 7) == 0) ? 1 : 0;
 
-  if (pl.live_map) {
-    uint8_t* map = (uint8_t*)p->workspace + pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
-    kp.live_map_out = map;
-    kp.map_row_bytes = pl.map_row_bytes;
-    kp.map_rows = pl.block_m / pl.pack;
+  // the live-tile map and the staged mask (workspace after the split
+  // partials and tickets)
+  kp.msrc = kp.mask; kp.msrc_bs = kp.m_bs; kp.msrc_rs = kp.m_rs; kp.msrc_q = kp.msq;
+  kp.map_row_bytes = pl.map_row_bytes;
+  kp.map_slices = pl.map_slices;
+  if (pl.live_map)
+    kp.live_map_out = (uint8_t*)p->workspace + pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
+  if (pl.staged) {
+    kp.stage_out = (uint16_t*)((char*)p->workspace + pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes +
+                               pl.map_bytes);
+    kp.stage_rs = pl.stage_rs;
+    kp.mask = kp.stage_out;
+    kp.m_rs = pl.stage_rs;
+    kp.m_bs = (int64_t)p->seqlen_q * pl.stage_rs;
+    kp.msq = p->seqlen_q;
+    kp.mask_direct = 1;
   }
 
   CParams cp{};
@@ -2497,7 +2608,9 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
   return MI355_FA_OK;
 }
 
-}  // extern "C"
+extern "C" int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errlen) {
+  return fwd_impl(p, stream, err, errlen, true);
+}
 
 // ── entry point that allocates nothing ───────────────────────────────────────
 // mi355_fa_fwd_noalloc keeps the split-KV partials in this file-scope device
@@ -2541,7 +2654,13 @@ extern "C" int mi355_fa_fwd_noalloc(const mi355_fa_params* p, void* stream, char
   int rc = validate(p, err, errlen);
   if (rc) return rc;
   if (p->b == 0 || p->h == 0 || p->seqlen_q == 0) return MI355_FA_OK;
-  const size_t need = mi355_fa_workspace_bytes(p);
+  // the staged mask when it fits the scratch, else the mask read in place
+  size_t need = mi355_fa_workspace_bytes(p);
+  bool allow_stage = true;
+  if (need > MI355_FA_NOALLOC_SCRATCH_BYTES) {
+    allow_stage = false;
+    need = make_plan(p, device_info().cus, false).ws_bytes;
+  }
   if (need > MI355_FA_NOALLOC_SCRATCH_BYTES) {
     set_err(err, errlen,
             "split-KV needs %zu bytes of scratch; mi355_fa_fwd_noalloc holds at most %zu "
@@ -2557,5 +2676,5 @@ extern "C" int mi355_fa_fwd_noalloc(const mi355_fa_params* p, void* stream, char
     if (rc) return rc;
     q.workspace_bytes = MI355_FA_NOALLOC_SCRATCH_BYTES;
   }
-  return mi355_fa_fwd(&q, stream, err, errlen);
+  return fwd_impl(&q, stream, err, errlen, allow_stage);
 }

@@ -11,9 +11,12 @@ Mirrors the reference's torch op (Defyli/custom_ops):
   * output ``empty_like(q)`` (fa_fwd_op.cu:141), scale 1/sqrt(d) (:186-188),
     launched on the current stream of q's device, no host sync (:191-194).
 
-Differences by design: Sk % 8 != 0 needs no padded copies (fa_fwd_op.cu:117-134
-pads K/V/mask); the HIP kernel predicates the tail in place. Split-KV partials
-come from the caching allocator as one workspace tensor sized by the library.
+Differences by design: Sk % 8 != 0 pads no K/V (fa_fwd_op.cu:117-134 pads
+K/V/mask); the HIP kernels predicate the key tail in place, and a mask whose
+rows are not 16-byte aligned is staged by a pre-pass into an aligned copy in
+the workspace (all launches but 8-wave split ones). Split-KV partials, the
+live-tile map and the staged mask come from the caching allocator as one
+workspace tensor sized by the library.
 """
 from __future__ import annotations
 

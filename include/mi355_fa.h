@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MI355_FA_ABI_VERSION 2
+#define MI355_FA_ABI_VERSION 3
 
 /* Error codes returned by the entry points (0 = success). */
 enum {
@@ -66,6 +66,9 @@ typedef struct mi355_fa_variant {
                         one workgroup of the launch)                               */
   int32_t live_map;  /* 0 | -1: masks with unaligned rows narrow by each workgroup's
                         own scan instead of the live-tile map pre-pass             */
+  int32_t stage;     /* 0 | 1 always | -1 never: masks with unaligned rows are read
+                        from an aligned staged copy in the workspace (default: all
+                        launches but 8-wave split ones) instead of in place        */
 } mi355_fa_variant;
 
 /*
@@ -103,8 +106,9 @@ typedef struct mi355_fa_params {
   /* Split-KV: 0 = let the library plan it; >= 1 forces that many splits. */
   int32_t num_splits;
   /* Device workspace for split-KV partials, the fused split tail's ticket
-   * words and the live-tile map of masks with unaligned rows (may be NULL when
-   * mi355_fa_workspace_bytes reports 0; its contents need no clearing). */
+   * words, and for masks with unaligned rows the live-tile map and an aligned
+   * staged copy of the mask (may be NULL when mi355_fa_workspace_bytes
+   * reports 0; its contents need no clearing). */
   void* workspace;
   size_t workspace_bytes;
   /* Test/tuning variant selection (NULL = the library's plan); see above. */
@@ -120,10 +124,11 @@ int mi355_fa_fwd(const mi355_fa_params* p, void* stream, char* err, size_t errle
 
 /* mi355_fa_fwd without any allocation and without a workspace argument: the
  * workspace contents (split-KV partials and tickets, the live-tile map of
- * masks with unaligned rows) go to a fixed per-GPU device array of
- * MI355_FA_NOALLOC_SCRATCH_BYTES (allocated when the library's code is loaded
- * onto a GPU and held until the process ends). p->workspace is ignored. Plans
- * that need more scratch fail with MI355_FA_EWORKSPACE. Calls that overlap on
+ * masks with unaligned rows and their staged copy) go to a fixed per-GPU
+ * device array of MI355_FA_NOALLOC_SCRATCH_BYTES (allocated when the
+ * library's code is loaded onto a GPU and held until the process ends).
+ * p->workspace is ignored. A staged mask that does not fit is read in place
+ * instead; plans that still need more scratch fail with MI355_FA_EWORKSPACE. Calls that overlap on
  * one GPU (other streams, other threads) share the array and race: serialise
  * them. No counterpart in the reference; it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
@@ -135,7 +140,8 @@ int mi355_fa_fwd_noalloc(const mi355_fa_params* p, void* stream, char* err, size
 int mi355_fa_num_splits(const mi355_fa_params* p);
 
 /* Bytes of workspace mi355_fa_fwd needs for these params (split partials and
- * tickets, the live-tile map of masks with unaligned rows; 0 when neither). */
+ * tickets; for masks with unaligned rows the live-tile map and the staged
+ * copy; 0 when none of these). */
 size_t mi355_fa_workspace_bytes(const mi355_fa_params* p);
 
 /* Pure cost model, exposed for host tests: splits for a problem of

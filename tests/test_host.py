@@ -30,7 +30,7 @@ def test_header_symbols_exported(lib):
     assert set(names) == set(_lib.EXPORTED)
     for n in names:
         assert hasattr(lib, n), f"{n} not exported"
-    assert lib.mi355_fa_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.mi355_fa_abi_version() == _lib.ABI_VERSION == 3
     assert b"gfx950" in lib.mi355_fa_build_info()
 
 

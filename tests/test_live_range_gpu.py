@@ -3,7 +3,9 @@ the last one in which its rows' mask has a visible entry, and the splits share
 that range): parity on masks with dead edges, for every tile-loop form, with
 narrowing forced on (``Variant(live=1)``) and off (``live=-1``), and, for
 masks whose rows are not 16-byte aligned, the live ranges from the pre-pass
-live-tile map against each workgroup's own scan (``live_map=-1``).
+live-tile map against each workgroup's own scan (``live_map=-1``), and the
+mask read from the pre-pass's aligned staged copy (``stage=1``) against the
+mask read in place (``stage=-1``).
 
   * every output against the fp32 torch restatement of the reference op
     (tests/test_mha_fwd_with_mask.py:38-53 of the reference) at the suite's
@@ -98,6 +100,8 @@ def test_live_range_parity(gpu, loop):
     from custom_ops_amd import Variant, mha_fwd_with_mask
     on, off = Variant(loop=loop, live=1), Variant(loop=loop, live=-1)
     scan = Variant(loop=loop, live=1, live_map=-1)   # unaligned rows: the scan instead of the map
+    # unaligned rows: the staged copy always / never (default: all but 8-wave split launches)
+    staged, inplace = Variant(loop=loop, live=1, stage=1), Variant(loop=loop, live=1, stage=-1)
     for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr) in enumerate(CASES):
         g = torch.Generator().manual_seed(1000 + n)
         q = (torch.randn(b, h, sq, d, generator=g) * 0.5).to(dt).cuda()
@@ -106,7 +110,8 @@ def test_live_range_parity(gpu, loop):
         m = mask_of(kind, b, sq, sk, sk + xc, sq + xr, g).to(dt).cuda()
         ref = ref_attn_torch(q, k, v, m[:, :, :sq, :sk])
         dead = torch.isinf(m[:, :, :sq, :sk].float()).all(-1)          # [b, 1, sq]
-        outs = [mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=var) for var in (on, off, scan)]
+        outs = [mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=var)
+                for var in (on, off, scan, staged, inplace)]
         torch.cuda.synchronize()
         # Unsplit, the map's exact range and the scan's (which may be wider: a
         # chunk read partly past the end of the mask counts as visible) give
@@ -115,7 +120,7 @@ def test_live_range_parity(gpu, loop):
         if splits == 1:
             assert torch.equal(outs[0].view(torch.int16), outs[2].view(torch.int16)), \
                 f"loop {loop} case {n} {kind}: live-tile map and scan differ"
-        for var, out in zip(("on", "off", "scan"), outs):
+        for var, out in zip(("on", "off", "scan", "staged", "in place"), outs):
             tag = f"loop {loop} live {var} case {n} {kind}"
             assert_close(out, ref, tag)
             assert bool((out.float().masked_select(dead.unsqueeze(-1).expand(b, h, sq, d)) == 0).all()), tag
@@ -137,46 +142,61 @@ MAP_CASES = [  # kind, b, h, hk, sq, sk, d, dtype, splits, extra mask cols, extr
 
 
 @pytest.mark.gpu
-def test_live_map_matches_host(gpu):
-    """The live-tile map itself, read back from the workspace (its last
-    region: ``[B][m-blocks][ceil(tiles / 8)]`` bytes rounded up to 256),
-    against the tiles that hold a visible entry of a row < Sq in a column < Sk,
-    recomputed on the host. Covers the chunk that holds Sk in the last row of
-    the mask, whose 16-byte load would reach past the buffer's end."""
+def test_live_map_and_staged_mask_match_host(gpu):
+    """The pre-pass outputs themselves, read back from the workspace (after the
+    split partials and tickets: the live-tile map, ``[B][ceil(Sq / 16)]
+    [ceil(tiles / 8)]`` bytes, then the staged mask ``[B][Sq][ceil8(Sk)]``,
+    each rounded up to 256 bytes), against the host: map bit t of slice r / 16
+    set exactly when tile t holds a visible entry of a row r < Sq of the slice
+    in a column < Sk; the staged mask equal to the mask's rows < Sq and
+    columns < Sk, -inf in the padding columns. Covers the chunk that holds Sk
+    in the last row of the mask, whose 16-byte load would reach past the
+    buffer's end."""
     import ctypes
     from custom_ops_amd import _lib, Variant
     from custom_ops_amd.fa import make_params
     lib = _lib.load()
+    r256 = lambda x: (x + 255) & ~255   # noqa: E731
     for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr, waves) in enumerate(MAP_CASES):
         g = torch.Generator().manual_seed(2000 + n)
         q = torch.randn(b, h, sq, d, generator=g).to(dt).cuda()
         k = torch.randn(b, hk, sk, d, generator=g).to(dt).cuda()
         m = mask_of(kind, b, sq, sk, sk + xc, sq + xr, g).to(dt).cuda()
         assert (sk + xc) % 8 != 0
-        out = torch.empty_like(q)
-        var = Variant(waves=waves, live=1)
-        p = make_params(q, k, k, m, out, splits, var)
-        nbytes = lib.mi355_fa_workspace_bytes(ctypes.byref(p))
-        ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
-        p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
-        err = ctypes.create_string_buffer(512)
-        rc = lib.mi355_fa_fwd(ctypes.byref(p), torch.cuda.current_stream().cuda_stream, err, 512)
-        assert rc == 0, err.value
-        torch.cuda.synchronize()
-        pack = 1
-        while pack * 2 <= 4 and (h // hk) % (pack * 2) == 0:
-            pack *= 2
-        rows = 32 * waves // pack
-        num_m, nn = -(-sq // rows), -(-sk // 64)
-        row_bytes = -(-nn // 8)
-        size = b * num_m * row_bytes
-        off = nbytes - ((size + 255) & ~255)
-        mp = ws[off: off + size].cpu().view(b, num_m, row_bytes)
-        vis = ~torch.isinf(m[:, 0, :sq, :sk].float().cpu())
-        for bb in range(b):
-            for rb in range(num_m):
-                rr = vis[bb, rb * rows: min(sq, (rb + 1) * rows)]
-                for t in range(nn):
-                    want = bool(rr[:, t * 64:(t + 1) * 64].any())
-                    got = bool((int(mp[bb, rb, t // 8]) >> (t % 8)) & 1)
-                    assert want == got, f"case {n} {kind}: batch {bb} row block {rb} tile {t}: map {got}"
+        for stage in (1, -1):
+            out = torch.empty_like(q)
+            var = Variant(waves=waves, live=1, stage=stage)
+            p = make_params(q, k, k, m, out, splits, var)
+            nbytes = lib.mi355_fa_workspace_bytes(ctypes.byref(p))
+            ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
+            p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+            err = ctypes.create_string_buffer(512)
+            rc = lib.mi355_fa_fwd(ctypes.byref(p), torch.cuda.current_stream().cuda_stream, err, 512)
+            assert rc == 0, err.value
+            torch.cuda.synchronize()
+            s_ = lib.mi355_fa_num_splits(ctypes.byref(p))
+            pack = 1
+            while pack * 2 <= 4 and (h // hk) % (pack * 2) == 0:
+                pack *= 2
+            num_m, nn, slices, skp = -(-sq // (32 * waves // pack)), -(-sk // 64), -(-sq // 16), -(-sk // 8) * 8
+            row_bytes = -(-nn // 8)
+            off = 0
+            if s_ > 1:
+                off = r256(s_ * b * h * sq * d * 2) + r256(s_ * b * h * sq * 4) + r256(b * (h // pack) * num_m * 8)
+            size = b * slices * row_bytes
+            stage_bytes = r256(b * sq * skp * 2) if stage == 1 else 0
+            assert nbytes == off + r256(size) + stage_bytes, (n, nbytes, off, size, stage_bytes)
+            mp = ws[off: off + size].cpu().view(b, slices, row_bytes)
+            vis = ~torch.isinf(m[:, 0, :sq, :sk].float().cpu())
+            for bb in range(b):
+                for sl in range(slices):
+                    rr = vis[bb, sl * 16: min(sq, sl * 16 + 16)]
+                    for t in range(nn):
+                        want = bool(rr[:, t * 64:(t + 1) * 64].any())
+                        got = bool((int(mp[bb, sl, t // 8]) >> (t % 8)) & 1)
+                        assert want == got, f"case {n} {kind} stage {stage}: batch {bb} slice {sl} tile {t}: map {got}"
+            if stage == 1:
+                st = ws[off + r256(size): off + r256(size) + b * sq * skp * 2].view(dt).cpu().view(b, sq, skp)
+                want = torch.full((b, sq, skp), NEG, dtype=dt)
+                want[:, :, :sk] = m[:, 0, :sq, :sk].cpu()
+                assert torch.equal(st.view(torch.int16), want.view(torch.int16)), f"case {n} {kind}: staged mask"
