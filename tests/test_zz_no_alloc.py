@@ -1,9 +1,10 @@
-"""mi355_fa_fwd_noalloc (split partials and the live-tile map of masks with
-unaligned rows in the library's per-GPU scratch array,
+"""mi355_fa_fwd_noalloc (split partials, and for masks with unaligned rows the
+live-tile map and the staged mask copy, in the library's per-GPU scratch array,
 no workspace, no allocation) against mi355_fa_fwd with a caller workspace, both
 called through the C-ABI: bit-identical outputs on two calls in a row (the
-second smaller, so stale scratch contents from the first must not leak in),
-and a clear rejection of a plan whose partials exceed the array.
+second smaller, so stale scratch contents from the first must not leak in), a
+staged copy too large for the array replaced by the mask read in place, and a
+clear rejection of a plan whose partials exceed the array.
 """
 import ctypes
 
@@ -29,10 +30,10 @@ def _inputs(b, h, hk, sq, sk, d, seed, dtype=torch.bfloat16):
     return q, k, v, mask
 
 
-def _run(entry, q, k, v, mask, splits):
+def _run(entry, q, k, v, mask, splits, variant=None):
     lib = _lib.load()
     out = torch.full_like(q, float("nan"))
-    p = make_params(q, k, v, mask, out, splits)
+    p = make_params(q, k, v, mask, out, splits, variant)
     ws = None
     if entry == "fwd":
         n = lib.mi355_fa_workspace_bytes(ctypes.byref(p))
@@ -59,7 +60,8 @@ def test_noalloc_matches_workspace_entry_two_calls(dtype):
         # the second is smaller and reuses it
         (1, 16, 16, 128, 16384, 128, 16, 11),
         (1, 4, 2, 100, 3001, 64, 5, 12),
-        # unsplit, unaligned mask rows: only the live-tile map in the array
+        # unsplit, unaligned mask rows: the staged mask (and no map: the
+        # assembly loop does not narrow unsplit launches) in the array
         (2, 4, 4, 300, 777, 128, 1, 13),
     ]
     for b, h, hk, sq, sk, d, splits, seed in cases:
@@ -77,6 +79,22 @@ def test_noalloc_unsplit_needs_no_scratch():
     got, _ = _run("noalloc", q, k, v, mask, 1)
     assert need == 0
     assert torch.equal(got, ref)
+
+
+def test_noalloc_reads_the_mask_in_place_when_the_copy_does_not_fit():
+    """[4, 1, 2048, 2047] staged is 32 MiB plus its padding: beyond the array,
+    so the no-allocation entry point plans without the copy, like
+    mi355_fa_fwd with Variant(stage=-1)."""
+    q, k, v, mask = _inputs(4, 2, 2, 2048, 2047, 128, 15)
+    lib = _lib.load()
+    p = make_params(q, k, v, mask, q, 1)
+    assert lib.mi355_fa_workspace_bytes(ctypes.byref(p)) > SCRATCH
+    ref, _ = _run("fwd", q, k, v, mask, 1, _lib.Variant(stage=-1))
+    got, _ = _run("noalloc", q, k, v, mask, 1)
+    assert not torch.isnan(ref).any()
+    assert torch.equal(got, ref)
+    staged, _ = _run("fwd", q, k, v, mask, 1)
+    assert (staged.float() - ref.float()).abs().max().item() < 2e-2
 
 
 def test_noalloc_rejects_plans_beyond_the_array():
