@@ -113,7 +113,7 @@ def is_combine(name: str) -> bool:
 
 
 def is_map(name: str) -> bool:
-    return "live_map_kernel" in name
+    return "mask_stage_kernel" in name   # the mask pre-pass (staged copy and/or live-tile map)
 
 
 def is_copy(name: str) -> bool:
@@ -355,7 +355,7 @@ def main() -> None:
 
     ours = [r for r in trace if "mi355fa::" in r["Kernel_Name"]]
     spans, i = [], 0
-    while i < len(ours):            # a call: [live_map] attention [combine]
+    while i < len(ours):            # a call: [mask pre-pass] attention [combine]
         j = i
         while j < len(ours) and not is_attn(ours[j]["Kernel_Name"]):
             j += 1
@@ -380,11 +380,11 @@ def main() -> None:
         "counted_launches": args.iters,
         "counted_avg_us": counted(is_attn),
         "counted_combine_avg_us": counted(is_combine) if comb else None,
-        "counted_live_map_avg_us": counted(is_map) if lmap else None,
+        "counted_mask_prepass_avg_us": counted(is_map) if lmap else None,
         "counted_call_span_us": sum(spans) / len(spans) if spans else None,
         "combine_avg_us": float(comb[0]["AverageNs"]) / 1e3 if comb else None,
-        "live_map_avg_us": float(lmap[0]["AverageNs"]) / 1e3 if lmap else None,
-        "live_map_fetch_bytes": fetch_map * f_fac * 1024 if (fetch_map and f_fac) else None,
+        "mask_prepass_avg_us": float(lmap[0]["AverageNs"]) / 1e3 if lmap else None,
+        "mask_prepass_fetch_bytes": fetch_map * f_fac * 1024 if (fetch_map and f_fac) else None,
         "combine_bytes": ((fetch_comb or 0) * f_fac + (write_comb or 0) * w_fac) * 1024
                          if (comb and f_fac and w_fac) else None,
         "achieved_tflops": cfg.flops / (avg_ns * 1e-9) / 1e12,
