@@ -212,6 +212,10 @@ struct KParams {
   const uint8_t* live_map;
   int map_row_bytes;         // bytes per slice: ceil(num_n / 8)
   int map_slices;            // slices per batch: ceil(Sq / 16)
+  // map_full_off bytes after the map: a byte per (batch, slice), 1 when tile 0
+  // and the last tile both hold a visible entry of the slice's rows (the row
+  // block's range is then the whole axis; its map bytes may be unwritten)
+  int64_t map_full_off;
   uint8_t* live_map_out;     // the same map, for mask_stage_kernel
   // The mask as the caller passed it, for mask_stage_kernel: with a staged
   // copy, mask / m_bs / m_rs / msq above describe the copy instead
@@ -485,11 +489,11 @@ __device__ __forceinline__ rsrc_t mask_rsrc(CKParams& p, int b) {
 
 struct LiveProbe { u32x4 l, r; };
 
-template <int NT, bool MAP = false>
+template <int NT, bool MAP = false, bool SCAN = true>
 __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams& pk) {
   CKParams& p = kernarg_params(pk);
   LiveProbe pr{};
-  if (!uni(p.live)) return pr;
+  if (!SCAN || !uni(p.live)) return pr;
   if constexpr (MAP) {
     if (p.live_map) return pr;
   }
@@ -521,6 +525,10 @@ __device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int row
       mhi = max(mhi, t0 + 32 - __builtin_clz(v));   // one past the last
     }
   }
+  // a slice flagged whole-axis: its bytes may be unwritten, the range is [0, num_n)
+  const uint8_t* full = p.live_map + p.map_full_off + (int64_t)ti.b * p.map_slices + s0;
+  for (int i = tid; i < s1 - s0; i += NT)
+    if (full[i]) { mlo = 0; mhi = p.num_n; }
   // per wave by DPP, then one slot per wave (no LDS atomics: the compiler's
   // whole-wave reduction for them needs registers the assembly loops lack)
   mlo = wave_min(mlo);
@@ -536,7 +544,8 @@ __device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int row
     mlo = min(mlo, w[2 * i]);
     mhi = max(mhi, w[2 * i + 1]);
   }
-  int lo = (int)__builtin_amdgcn_readfirstlane(mlo), hi = (int)__builtin_amdgcn_readfirstlane(mhi) - 1;
+  int lo = (int)__builtin_amdgcn_readfirstlane(mlo);
+  int hi = min((int)__builtin_amdgcn_readfirstlane(mhi), p.num_n) - 1;
   __syncthreads();                         // every wave has read `red` before any DMA lands
   if (lo > hi) { lo = 0; hi = -1; }        // no visible entry in these rows
   if (lo == 0 && hi == p.num_n - 1) return false;   // whole axis live: the nominal ranges stand
@@ -592,6 +601,31 @@ __global__ __launch_bounds__(256) void mask_stage_kernel(KParams p) {
   const rsrc_t rm = make_rsrc(reinterpret_cast<const void*>(abase), nrec);
   const int sk = p.sk;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint8_t* full_out = p.live_map_out ? p.live_map_out + p.map_full_off + (int64_t)b * p.map_slices + sl : nullptr;
+  if (!p.stage_out) {
+    // Map only: first a probe of the slice's rows in tile 0 (lanes k = 0-7 of
+    // each 16) and in the last tile (k = 8-15; the chunk that holds Sk read
+    // shifted back to end at column Sk - 1). Both live: the row block's range
+    // is the whole axis, so the flag says so and the 8 tiles need no reading
+    // (a dense mask reads 2 tiles per row). Every group's workgroup of the
+    // slice computes the same flag.
+    const int t = threadIdx.x, row = t >> 4, k = t & 15;
+    const int c0 = (k < 8 ? 0 : (p.num_n - 1) * kBN) + 8 * (k & 7);
+    const bool in = row < nr && c0 < sk;
+    const int sh = max(c0 + 8 - sk, 0);
+    const uint32_t off = lead + ((uint32_t)(r0 + row) * (uint32_t)p.msrc_rs + (uint32_t)(c0 - sh)) * 2u;
+    const u32x4 pv = bload16(rm, in ? off : 0xfffffff0u);
+    bool live = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      live |= (j >= sh) & (((pv[j >> 1] >> (16 * (j & 1))) & 0xffffu) != kNeg);
+    live &= in;
+    const bool l0 = __syncthreads_or(live && k < 8), l1 = __syncthreads_or(live && k >= 8);
+    if (threadIdx.x == 0) *full_out = (l0 && l1) ? 1u : 0u;
+    if (l0 && l1) return;
+  } else if (full_out && threadIdx.x == 0) {
+    *full_out = 0u;
+  }
   u32x4 v[kSteps], x[kSteps];
   uint32_t dl[kSteps];
 #pragma unroll
@@ -650,7 +684,38 @@ __global__ __launch_bounds__(256) void mask_stage_kernel(KParams p) {
     p.live_map_out[((int64_t)b * p.map_slices + sl) * p.map_row_bytes + g] = (uint8_t)bits;
 }
 
-template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool MAP = false>
+// range_from_map for the assembly loops: every wave reads its row block's map
+// bytes itself and reduces them by DPP (no LDS, no barrier, few SGPRs).
+__device__ __forceinline__ bool range_from_map_wave(TileIdx& ti, CKParams& p, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int nbytes = p.map_row_bytes;
+  const int s0 = ti.m0 >> 4, s1 = min((ti.m0 + rows + 15) >> 4, p.map_slices);
+  const uint8_t* map = p.live_map + ((int64_t)ti.b * p.map_slices + s0) * nbytes;
+  int mlo = 0x7fffffff, mhi = 0;
+  for (int i = lane; i < (s1 - s0) * nbytes; i += 64) {
+    const uint32_t v = map[i];
+    if (v) {
+      const int t0 = (i % nbytes) * 8;
+      mlo = min(mlo, t0 + __builtin_ctz(v));
+      mhi = max(mhi, t0 + 32 - __builtin_clz(v));   // one past the last
+    }
+  }
+  // a slice flagged whole-axis: its bytes may be unwritten, the range is [0, num_n)
+  const uint8_t* full = p.live_map + p.map_full_off + (int64_t)ti.b * p.map_slices + s0;
+  for (int i = lane; i < s1 - s0; i += 64)
+    if (full[i]) { mlo = 0; mhi = p.num_n; }
+  int lo = wave_min(mlo), hi = min(wave_max(mhi), p.num_n) - 1;
+  if (lo > hi) { lo = 0; hi = -1; }        // no visible entry in these rows
+  if (lo == 0 && hi == p.num_n - 1) return false;   // whole axis live: the nominal ranges stand
+  const int ns = p.num_splits;
+  const int per = (hi - lo + 1 + ns - 1) / ns;
+  const int nb = min(lo + ti.split * per, hi + 1);
+  ti.nb = nb;
+  ti.ne = min(nb + per, hi + 1);
+  return true;
+}
+
+template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool MAP = false, bool SCAN = true>
 __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, int rows, const LiveProbe& pr,
                                                uint32_t* red) {
   CKParams& p = kernarg_params(pk);
@@ -660,8 +725,12 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   const int tid = threadIdx.x;
   const int nn = p.num_n;   // the scan's control stays in VGPRs: no SGPRs to spare here
   if constexpr (MAP) {
-    if (p.live_map) return range_from_map<NT>(ti, p, rows, red);
+    if (p.live_map) {
+      if constexpr (REUSE) return range_from_map<NT>(ti, p, rows, red);
+      else return range_from_map_wave(ti, p, rows);
+    }
   }
+  if constexpr (!SCAN) return false;
   // the probe's verdict: tile 0 / tile nn - 1 live in the chunks it read
   uint32_t lb = ((tid < nr * 8) & live8<BF16>(pr.l, (tid & 7) * 8, p.sk)) ? 1u : 0u;
   uint32_t rb = ((tid < nr * 8) & live8<BF16>(pr.r, (nn - 1) * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
@@ -1426,7 +1495,7 @@ struct Attn {
 // most one workgroup per CU): a third K/V stage, in dynamic LDS, so the
 // compiler still budgets registers for two waves per SIMD (static LDS past
 // 80 KiB would lift that target and cost AGPR copies in the tile loop).
-template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES, bool DEEP>
+template <int D, bool BF16, bool SPLIT, bool MDIRECT, int WAVES, bool DEEP, bool MAPONLY = false>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel(const KParams p) {
   typedef Geo<D, WAVES> G;
@@ -1456,13 +1525,15 @@ void fa_fwd_kernel(const KParams p) {
   static_assert(kTailOwn || !SPLIT || kTailFloats * 4 <= NSS * G::kVElems * 2, "tail fits in the V stages");
   __shared__ __align__(16) float sTail[kTailOwn ? kTailFloats : 1];
 
-  // Live ranges from the live-tile map: every kernel but the 4-wave deep ones
-  // on the LDS-DMA mask path, whose SGPRs it would push into spills (they
-  // scan)
-  constexpr bool kMap = !MDIRECT || WAVES == 8 || !DEEP;
+  // Live ranges from the live-tile map or the probe and scan: both in one
+  // kernel, but the 4-wave deep ones on the LDS-DMA mask path, whose SGPRs
+  // the two together would push into spills, have one instance each
+  // (MAPONLY: the map, launched when the launch has one)
+  constexpr bool kMap = MAPONLY || !MDIRECT || WAVES == 8 || !DEEP;
+  constexpr bool kScan = !MAPONLY;
   TileIdx ti = tile_index<G::kBM>(p);
   const TileIdx tg = ti;   // the workgroup's first head and row
-  const LiveProbe lp = live_probe<G::kThreads, kMap>(tg, p);
+  const LiveProbe lp = live_probe<G::kThreads, kMap, kScan>(tg, p);
   place_wave(ti, p, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), 32);
   A a(p);
   a.init(ti);
@@ -1497,7 +1568,7 @@ void fa_fwd_kernel(const KParams p) {
   {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
-    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, kMap>(tn, p, G::kBM / p.pack, lp,
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, kMap, kScan>(tn, p, G::kBM / p.pack, lp,
                                                        reinterpret_cast<uint32_t*>(KS(NST - 1)))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
@@ -1794,14 +1865,19 @@ constexpr int kPpVBase = 3 * kPpKStage;
 constexpr int kPpMBase = 6 * kPpKStage;
 constexpr int kPpLds = kPpMBase + 2 * 32768;    // 160 KiB
 
-template <bool SPLIT>
+// MAPPED: the live ranges come from the live-tile map (a launch that has
+// one), else from the probe and scan; the two are separate instances because
+// both in one push the prologue's SGPRs past what the allocator can spill.
+template <bool SPLIT, bool MAPPED>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_fwd_kernel_pp(const KParams p) {
   constexpr int D = 128;
   constexpr int UPR = D / 8;
   __shared__ __align__(16) uint8_t smem[kPpLds];
   TileIdx ti = tile_index<256>(p);
-  {
+  if constexpr (MAPPED) {
+    if (uni(kernarg_params(p).live)) range_from_map_wave(ti, kernarg_params(p), 256 / p.pack);
+  } else {
     // before the set-up below: its values would be live across the scan, and
     // the SGPRs the scan needs on top of them would spill
     const LiveProbe lp = live_probe<512>(ti, p);
@@ -2144,6 +2220,7 @@ struct Plan {
   int kv_nt;           // every K/V tile is read by one workgroup: non-temporal loads
   int live_map;        // a live-tile map pre-pass serves the live ranges (unaligned mask rows)
   int map_row_bytes, map_slices;
+  int64_t map_full_off;
   size_t map_bytes;
   int staged;          // unaligned mask rows copied to an aligned staged mask
   int stage_rs;
@@ -2280,10 +2357,22 @@ static Plan make_plan(const mi355_fa_params* p, int cus, bool allow_stage = true
   {
     const bool mask_direct = ((uintptr_t)p->mask & 15) == 0 && (p->mask_batch_stride & 7) == 0 &&
                              (p->mask_row_stride & 7) == 0;
-    pl.live_map = !mask_direct && pl.live != 0 && pl.num_n >= 4 && v.live_map >= 0;
+    // The map also serves 8-wave split launches of aligned masks, whose
+    // workgroups would otherwise each scan their rows' dead mask: with the
+    // heads and splits that share a row block, a window or causal mask reads
+    // its dead part dozens of times ([2,16,16,1000,4096] window 122.8 -> 47.2
+    // µs, top-left causal [2,16,4,1000,4096] 55.2 -> 37.0) while a dense mask
+    // pays the pre-pass (78.5 -> 81.4). 4-wave deep launches (one workgroup
+    // per CU, split-KV decode shapes such as cfg4) keep the scan: there the
+    // pre-pass is pure latency on a dense mask (4.4 µs, cfg4 +6 %), however
+    // many times a sparse one is re-read; Variant(live_map=1) forces the map.
+    pl.live_map = (!mask_direct || v.live_map > 0 || (s > 1 && pl.waves == 8)) && pl.live != 0 &&
+                  pl.num_n >= 4 && v.live_map >= 0;
     pl.map_row_bytes = ceil_div(pl.num_n, 8);
     pl.map_slices = ceil_div(p->seqlen_q, 16);
-    pl.map_bytes = pl.live_map ? (((size_t)p->b * pl.map_slices * pl.map_row_bytes + 255) & ~(size_t)255) : 0;
+    pl.map_full_off = (int64_t)(((size_t)p->b * pl.map_slices * pl.map_row_bytes + 255) & ~(size_t)255);
+    pl.map_bytes = pl.live_map ? (size_t)pl.map_full_off + (((size_t)p->b * pl.map_slices + 255) & ~(size_t)255)
+                               : 0;
     pl.stage_rs = ceil_div(p->seqlen_k, 8) * 8;
     // Staged by default except for 8-wave split launches, which run the
     // compiled kernel either way: there the copy's writes cost what the LDS
@@ -2367,7 +2456,10 @@ template <int D, bool BF16, bool SPLIT, int WAVES, bool DEEP>
 static hipError_t launch_main(const KParams& kp, hipStream_t st) {
   constexpr int NST = WAVES == 8 ? MI355_FA_STAGES8 : (DEEP && MI355_FA_STAGES4 < 3 ? 3 : MI355_FA_STAGES4);
   const size_t dyn = DEEP ? (size_t)(NST - 2) * (Geo<D, WAVES>::kKElems + Geo<D, WAVES>::kVElems) * 2 : 0;
-  if (kp.mask_direct)
+  if (kp.mask_direct && WAVES == 4 && DEEP && kp.live_map)
+    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, true, WAVES, DEEP, true>), dim3(kp.total),
+                       dim3(64 * WAVES), dyn, st, kp);
+  else if (kp.mask_direct)
     hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, SPLIT, true, WAVES, DEEP>), dim3(kp.total),
                        dim3(64 * WAVES), dyn, st, kp);
   else
@@ -2413,7 +2505,10 @@ static hipError_t launch_variant(const KParams& kp, const Plan& pl, hipStream_t 
   if constexpr (D == 128) {
     if (runs_asm_loop<D, BF16>(kp, pl)) {
       if (pl.loop == 3 && BF16)
-        hipLaunchKernelGGL((fa_fwd_kernel_pp<SPLIT>), dim3(kp.total), dim3(512), 0, st, kp);
+        if (kp.live_map)
+          hipLaunchKernelGGL((fa_fwd_kernel_pp<SPLIT, true>), dim3(kp.total), dim3(512), 0, st, kp);
+        else
+          hipLaunchKernelGGL((fa_fwd_kernel_pp<SPLIT, false>), dim3(kp.total), dim3(512), 0, st, kp);
       else if (pl.loop == 2)
         hipLaunchKernelGGL((fa_fwd_kernel_asm<2, BF16, SPLIT>), dim3(kp.total), dim3(256), 0, st, kp);
       else
@@ -2563,6 +2658,7 @@ static int fwd_impl(const mi355_fa_params* p, void* stream, char* err, size_t er
   kp.msrc = kp.mask; kp.msrc_bs = kp.m_bs; kp.msrc_rs = kp.m_rs; kp.msrc_q = kp.msq;
   kp.map_row_bytes = pl.map_row_bytes;
   kp.map_slices = pl.map_slices;
+  kp.map_full_off = pl.map_full_off;
   if (pl.live_map)
     kp.live_map_out = (uint8_t*)p->workspace + pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes;
   if (pl.staged) {

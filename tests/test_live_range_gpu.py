@@ -145,11 +145,13 @@ MAP_CASES = [  # kind, b, h, hk, sq, sk, d, dtype, splits, extra mask cols, extr
 def test_live_map_and_staged_mask_match_host(gpu):
     """The pre-pass outputs themselves, read back from the workspace (after the
     split partials and tickets: the live-tile map, ``[B][ceil(Sq / 16)]
-    [ceil(tiles / 8)]`` bytes, then the staged mask ``[B][Sq][ceil8(Sk)]``,
-    each rounded up to 256 bytes), against the host: map bit t of slice r / 16
-    set exactly when tile t holds a visible entry of a row r < Sq of the slice
-    in a column < Sk; the staged mask equal to the mask's rows < Sq and
-    columns < Sk, -inf in the padding columns. Covers the chunk that holds Sk
+    [ceil(tiles / 8)]`` bytes, its whole-axis flags ``[B][ceil(Sq / 16)]``,
+    then the staged mask ``[B][Sq][ceil8(Sk)]``, each rounded up to 256
+    bytes), against the host: map bit t of slice r / 16 set exactly when tile
+    t holds a visible entry of a row r < Sq of the slice in a column < Sk
+    (slices flagged whole-axis excepted: the flag is set exactly when tile 0
+    and the last tile both hold one); the staged mask equal to the mask's
+    rows < Sq and columns < Sk, -inf in the padding columns. Covers the chunk that holds Sk
     in the last row of the mask, whose 16-byte load would reach past the
     buffer's end."""
     import ctypes
@@ -184,19 +186,59 @@ def test_live_map_and_staged_mask_match_host(gpu):
             if s_ > 1:
                 off = r256(s_ * b * h * sq * d * 2) + r256(s_ * b * h * sq * 4) + r256(b * (h // pack) * num_m * 8)
             size = b * slices * row_bytes
+            map_bytes = r256(size) + r256(b * slices)
             stage_bytes = r256(b * sq * skp * 2) if stage == 1 else 0
-            assert nbytes == off + r256(size) + stage_bytes, (n, nbytes, off, size, stage_bytes)
+            assert nbytes == off + map_bytes + stage_bytes, (n, nbytes, off, size, stage_bytes)
             mp = ws[off: off + size].cpu().view(b, slices, row_bytes)
+            full = ws[off + r256(size): off + r256(size) + b * slices].cpu().view(b, slices)
             vis = ~torch.isinf(m[:, 0, :sq, :sk].float().cpu())
             for bb in range(b):
                 for sl in range(slices):
                     rr = vis[bb, sl * 16: min(sq, sl * 16 + 16)]
+                    ends = bool(rr[:, :64].any()) and bool(rr[:, (nn - 1) * 64:].any())
+                    # staged: the map is complete and no slice is flagged; in
+                    # place: a slice whose rows hold visible entries in tile 0
+                    # and in the last tile is flagged and its bytes skipped
+                    assert int(full[bb, sl]) == (0 if stage == 1 else int(ends)), (n, kind, stage, bb, sl)
+                    if int(full[bb, sl]):
+                        continue
                     for t in range(nn):
                         want = bool(rr[:, t * 64:(t + 1) * 64].any())
                         got = bool((int(mp[bb, sl, t // 8]) >> (t % 8)) & 1)
                         assert want == got, f"case {n} {kind} stage {stage}: batch {bb} slice {sl} tile {t}: map {got}"
             if stage == 1:
-                st = ws[off + r256(size): off + r256(size) + b * sq * skp * 2].view(dt).cpu().view(b, sq, skp)
+                st = ws[off + map_bytes: off + map_bytes + b * sq * skp * 2].view(dt).cpu().view(b, sq, skp)
                 want = torch.full((b, sq, skp), NEG, dtype=dt)
                 want[:, :, :sk] = m[:, 0, :sq, :sk].cpu()
                 assert torch.equal(st.view(torch.int16), want.view(torch.int16)), f"case {n} {kind}: staged mask"
+
+
+@pytest.mark.gpu
+def test_live_map_on_aligned_split_launches(gpu):
+    """Aligned masks: the map serves 8-wave split launches by default and the
+    4-wave deep ones (split-KV decode shapes) when forced
+    (``Variant(live_map=1)``: the map-only kernel instance); every output
+    against the fp32 restatement, and the map's ranges against the scan's
+    (``live_map=-1``) within the tolerance (split launches partition them)."""
+    from custom_ops_amd import Variant, mha_fwd_with_mask
+    cases = [  # kind, b, h, hk, sq, sk, waves, splits
+        ("causal", 1, 8, 8, 128, 8192, 4, 8),
+        ("pad", 1, 8, 2, 128, 8192, 4, 16),
+        ("window", 2, 8, 2, 700, 4096, 8, 2),
+        ("causal", 2, 8, 8, 500, 4096, 8, 3),
+    ]
+    for n, (kind, b, h, hk, sq, sk, waves, splits) in enumerate(cases):
+        g = torch.Generator().manual_seed(3000 + n)
+        q = (torch.randn(b, h, sq, 128, generator=g) * 0.5).bfloat16().cuda()
+        k = (torch.randn(b, hk, sk, 128, generator=g) * 0.5).bfloat16().cuda()
+        v = (torch.randn(b, hk, sk, 128, generator=g) * 0.5).bfloat16().cuda()
+        m = mask_of(kind, b, sq, sk, sk, sq, g).bfloat16().cuda()
+        ref = ref_attn_torch(q, k, v, m)
+        dead = torch.isinf(m.float()).all(-1)
+        for label, var in (("map", Variant(waves=waves, live_map=1)), ("default", Variant(waves=waves)),
+                           ("scan", Variant(waves=waves, live_map=-1))):
+            out = mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=var)
+            torch.cuda.synchronize()
+            tag = f"case {n} {kind} {label}"
+            assert_close(out, ref, tag)
+            assert bool((out.float().masked_select(dead.unsqueeze(-1).expand(b, h, sq, 128)) == 0).all()), tag
