@@ -581,8 +581,9 @@ __device__ __forceinline__ bool range_from_map(TileIdx& ti, CKParams& p, int row
 // batch's first entry to the one that holds its last: those lie in the pages
 // of the mask's own bytes, and no load reaches past the descriptor (a load
 // that does reads 0 for its in-range bytes too, and 0 is visible). Entries of
-// columns >= Sk and rows >= Sq are not counted and are staged as -inf. Every
-// map byte and every staged chunk has one writer, so neither needs clearing.
+// columns >= Sk and rows >= Sq are not counted; rows >= Sq are not staged, and
+// the staged columns Sk .. stage_rs - 1 hold -inf. Every map byte and every
+// staged chunk has one writer, so neither needs clearing.
 template <bool BF16>
 __global__ __launch_bounds__(256) void mask_stage_kernel(KParams p) {
   constexpr uint32_t kNegPair = BF16 ? 0xff80ff80u : 0xfc00fc00u;
