@@ -2526,7 +2526,10 @@ static hipError_t launch(const KParams& kp_in, const CParams& cp, const Plan& pl
   KParams kp = kp_in;
   const int lm = pl.live;
   kp.live = pl.num_n >= 4 && (lm == 1 || (lm == 2 && (pl.splits > 1 || !runs_asm_loop<D, BF16>(kp, pl))));
-  const bool want_map = kp.live && kp.live_map_out;
+  // the kernels that read the map: the compiled kernel and the ping-pong loop
+  // (the 32- and 64-row loops scan)
+  const bool reads_map = !runs_asm_loop<D, BF16>(kp, pl) || (D == 128 && BF16 && pl.loop == 3);
+  const bool want_map = kp.live && kp.live_map_out && reads_map;
   if (kp.stage_out || want_map) {
     KParams km = kp;
     if (!want_map) km.live_map_out = nullptr;
