@@ -489,7 +489,7 @@ __device__ __forceinline__ rsrc_t mask_rsrc(CKParams& p, int b) {
 
 struct LiveProbe { u32x4 l, r; };
 
-template <int NT, bool MAP = false, bool SCAN = true>
+template <int NT, bool MAP = false, bool SCAN = true, bool LOCAL = false>
 __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams& pk) {
   CKParams& p = kernarg_params(pk);
   LiveProbe pr{};
@@ -500,8 +500,10 @@ __device__ __forceinline__ LiveProbe live_probe(const TileIdx& ti, const KParams
   const rsrc_t rm = mask_rsrc(p, ti.b);
   const int tid = threadIdx.x;
   const uint32_t rowoff = (uint32_t)(ti.m0 + (tid >> 3)) * (uint32_t)p.m_rs + (uint32_t)(tid & 7) * 8u;
-  pr.l = bload16(rm, rowoff * 2u);
-  pr.r = bload16(rm, (rowoff + (uint32_t)(p.num_n - 1) * kBN) * 2u);
+  // LOCAL: the ends of the workgroup's own split range, else of the key axis
+  const int t0 = LOCAL ? ti.nb : 0, t1 = LOCAL ? max(ti.ne - 1, 0) : p.num_n - 1;
+  pr.l = bload16(rm, (rowoff + (uint32_t)t0 * kBN) * 2u);
+  pr.r = bload16(rm, (rowoff + (uint32_t)t1 * kBN) * 2u);
   return pr;
 }
 
@@ -716,7 +718,13 @@ __device__ __forceinline__ bool range_from_map_wave(TileIdx& ti, CKParams& p, in
   return true;
 }
 
-template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool MAP = false, bool SCAN = true>
+// LOCAL (the compiled kernel): a split launch without a map narrows each
+// workgroup's own nominal range [nb, ne) to its live tiles and keeps the
+// nominal partition, so a workgroup scans only its own share of the mask.
+// Scanning the whole axis to re-partition the live range (the assembly
+// loops) reads a sparse mask's dead part once per split and head: a top-left
+// causal [1,16,16,128,32768] took 357 µs that way on 16 splits.
+template <bool BF16, int NT, int BMAX, int J, bool REUSE, bool MAP = false, bool SCAN = true, bool LOCAL = false>
 __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, int rows, const LiveProbe& pr,
                                                uint32_t* red) {
   CKParams& p = kernarg_params(pk);
@@ -732,15 +740,18 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
     }
   }
   if constexpr (!SCAN) return false;
-  // the probe's verdict: tile 0 / tile nn - 1 live in the chunks it read
-  uint32_t lb = ((tid < nr * 8) & live8<BF16>(pr.l, (tid & 7) * 8, p.sk)) ? 1u : 0u;
-  uint32_t rb = ((tid < nr * 8) & live8<BF16>(pr.r, (nn - 1) * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
+  // the scanned range: the workgroup's own (LOCAL) or the whole key axis
+  const int first = LOCAL ? ti.nb : 0, last = LOCAL ? ti.ne - 1 : nn - 1;
+  if (LOCAL && first > last) return false;   // an empty share stays empty
+  // the probe's verdict: tile first / tile last live in the chunks it read
+  uint32_t lb = ((tid < nr * 8) & live8<BF16>(pr.l, first * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
+  uint32_t rb = ((tid < nr * 8) & live8<BF16>(pr.r, last * kBN + (tid & 7) * 8, p.sk)) ? 1u : 0u;
   wg_or2<NT>(lb, rb, red, 1);
-  if (lb && rb) {                          // whole axis live: the nominal ranges stand
+  if (lb && rb) {                          // both ends live: the nominal ranges stand
     __syncthreads();                       // every wave has read `red` before any DMA lands
     return false;
   }
-  int lo = lb ? 0 : -1, hi = rb ? nn - 1 : -1;
+  int lo = lb ? first : -1, hi = rb ? last : -1;
   constexpr int kRounds = (8 * BMAX + J * NT - 1) / (J * NT);   // rounds that cover one whole tile
   constexpr int NL = kRounds * J;
   const int cpt = nr * 8;                  // 16-byte chunks per tile of these rows
@@ -759,7 +770,7 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
   }
   const int c0 = (tid & 7) * 8;   // NT and cpt are multiples of 8: rem & 7 == tid & 7
   const int sk = p.sk;
-  int L = 0, R = nn - 1;
+  int L = first, R = last;
   for (int step = 0; lo < 0 || hi < 0; ++step) {
     if (L > R) break;                      // every tile scanned and dead
     // Two windows of U tile slots. While both ends are open, slots A read
@@ -806,6 +817,12 @@ __device__ __forceinline__ bool narrow_to_live(TileIdx& ti, const KParams& pk, i
     }
   }
   __syncthreads();                         // every wave has read `red` before any DMA lands
+  if constexpr (LOCAL) {
+    if (lo < 0) { lo = first; hi = first - 1; }   // no visible entry: an empty range
+    ti.nb = lo;
+    ti.ne = hi + 1;
+    return true;
+  }
   // no visible entry in these rows: an empty range (lo = 0, hi = -1)
   if (lo < 0) { lo = 0; hi = -1; }
   const int ns = uni(p.num_splits);
@@ -1534,7 +1551,7 @@ void fa_fwd_kernel(const KParams p) {
   constexpr bool kScan = !MAPONLY;
   TileIdx ti = tile_index<G::kBM>(p);
   const TileIdx tg = ti;   // the workgroup's first head and row
-  const LiveProbe lp = live_probe<G::kThreads, kMap, kScan>(tg, p);
+  const LiveProbe lp = live_probe<G::kThreads, kMap, kScan, SPLIT>(tg, p);
   place_wave(ti, p, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), 32);
   A a(p);
   a.init(ti);
@@ -1569,7 +1586,7 @@ void fa_fwd_kernel(const KParams p) {
   {
     // the last K stage is not loaded before the loop's first barrier
     TileIdx tn = tg;
-    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, kMap, kScan>(tn, p, G::kBM / p.pack, lp,
+    if (narrow_to_live<BF16, G::kThreads, G::kBM, 8, true, kMap, kScan, SPLIT>(tn, p, G::kBM / p.pack, lp,
                                                        reinterpret_cast<uint32_t*>(KS(NST - 1)))) {
       // the range moved: the first tiles again, for its first tile
       nb = tn.nb;
