@@ -242,3 +242,26 @@ def test_live_map_on_aligned_split_launches(gpu):
             tag = f"case {n} {kind} {label}"
             assert_close(out, ref, tag)
             assert bool((out.float().masked_select(dead.unsqueeze(-1).expand(b, h, sq, 128)) == 0).all()), tag
+
+
+@pytest.mark.gpu
+def test_local_scan_keeps_split_results(gpu):
+    """The compiled kernel's split launches without a map narrow each split's
+    own share and keep the nominal partition: every split runs the same live
+    tiles as without narrowing, so the outputs are bit for bit those of
+    ``live=-1``."""
+    from custom_ops_amd import Variant, mha_fwd_with_mask
+    on, off = Variant(loop=-1, live=1, live_map=-1), Variant(loop=-1, live=-1)
+    for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr) in enumerate(CASES):
+        if splits <= 1:
+            continue
+        g = torch.Generator().manual_seed(4000 + n)
+        q = (torch.randn(b, h, sq, d, generator=g) * 0.5).to(dt).cuda()
+        k = (torch.randn(b, hk, sk, d, generator=g) * 0.5).to(dt).cuda()
+        v = (torch.randn(b, hk, sk, d, generator=g) * 0.5).to(dt).cuda()
+        m = mask_of(kind, b, sq, sk, sk + xc, sq + xr, g).to(dt).cuda()
+        a = mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=on)
+        c = mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=off)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), c.view(torch.int16)), f"case {n} {kind}"
+        assert_close(a, ref_attn_torch(q, k, v, m[:, :, :sq, :sk]), f"case {n} {kind}")
