@@ -176,7 +176,8 @@ def cpu_baseline(seconds: float, reps: int = 5):
         "sample": f"cfg2: {base['heads_per_rep']} whole (b,h) heads per repetition, median of "
                   f"{reps} repetitions after an untimed one (spread {base['spread_pct']}%), fp32 "
                   f"torch math attention (scores+mask, guarded softmax, P@V) on {_cpu_name()}, "
-                  f"{cores} threads pinned to {cores} cores, extrapolated to the 64 heads",
+                  f"{cores} threads pinned to {cores} cores"
+                  + (", extrapolated to the 64 heads" if base["extrapolated"] else ", all 64 heads timed"),
         "us_full_workload": base["us"],
         "configs": out,
     }
