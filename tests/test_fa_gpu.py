@@ -602,6 +602,66 @@ def test_random_fuzz_vs_reference(ops, gpu):
             assert torch.all(out.permute(0, 2, 1, 3)[dead] == 0), str(case)
 
 
+def test_random_fuzz_variants_vs_reference(ops, gpu):
+    """300 seeded random cases as above, each with a random kernel variant and
+    split count: the staged mask copy forced on or off, the live-tile map
+    forced on or off, live-range narrowing forced on, the compiled kernel, 4-
+    or 8-wave workgroups, 2-7 splits; plus key-padding masks (a dead tail of
+    random length per batch) and masks with periodic dead tile runs. Every
+    output within the fp32 reference's tolerance, rows with no visible key
+    exactly 0."""
+    import random
+    from custom_ops_amd import Variant, mha_fwd_with_mask
+    rng = random.Random(11)
+    variants = [None, Variant(stage=1), Variant(stage=-1), Variant(live_map=1), Variant(live_map=-1),
+                Variant(live=1), Variant(loop=-1), Variant(waves=4), Variant(waves=8),
+                Variant(waves=4, live_map=1), Variant(loop=-1, live_map=-1, live=1)]
+    for i in range(300):
+        b = rng.choice([1, 1, 2, 3]); hk = rng.choice([1, 2, 4]); h = hk * rng.choice([1, 2, 4, 8])
+        sq = rng.choice([1, 7, 33, 64, 100, 128, 255, 257, 600, 1000, 2048])
+        sk = rng.choice([1, 9, 63, 64, 65, 300, 500, 1023, 1024, 1500, 2051, 4099, 9000, 16387])
+        if b * h * sq * sk > 6e7:
+            sk = max(1, int(6e7 // (b * h * sq)))
+        d = rng.choice([64, 128]); dt = rng.choice([torch.bfloat16, torch.float16])
+        er = rng.choice([0, 0, 3]); ec = rng.choice([0, 0, 0, 5, 8])
+        kind = rng.choice(["rand", "causal", "bias", "window", "rows", "pad", "holes", "dense"])
+        splits = rng.choice([0, 0, 0, 2, 3, 7])
+        var = rng.choice(variants)
+        g = torch.Generator(device=gpu).manual_seed(5000 + i)
+        q = (torch.randn(b, h, sq, d, generator=g, device=gpu) * 0.6).to(dt)
+        k = (torch.randn(b, hk, sk, d, generator=g, device=gpu) * 0.6).to(dt)
+        v = (torch.randn(b, hk, sk, d, generator=g, device=gpu) * 0.6).to(dt)
+        m = torch.zeros(b, 1, sq + er, sk + ec, device=gpu)
+        r = torch.arange(sq + er, device=gpu).view(-1, 1)
+        c = torch.arange(sk + ec, device=gpu).view(1, -1)
+        if kind == "rand":
+            m.masked_fill_(torch.rand(m.shape, generator=g, device=gpu) < 0.2, float("-inf"))
+        elif kind == "causal":
+            m.masked_fill_(c > r + (sk - sq), float("-inf"))
+        elif kind == "bias":
+            m += torch.randn(m.shape, generator=g, device=gpu) * 2.0
+        elif kind == "window":
+            off = r + (sk - sq)
+            m.masked_fill_((c > off) | (c <= off - rng.choice([64, 300, 1000])), float("-inf"))
+        elif kind == "pad":
+            for bb in range(b):
+                m[bb, :, :, rng.randint(0, sk):] = float("-inf")
+        elif kind == "holes":
+            m.masked_fill_(((c // 64) % 3 == 1) | ((c // 200) % 2 == 0), float("-inf"))
+        elif kind == "rows":
+            m[:, :, ::7, :] = float("-inf")
+        if ec:
+            m[..., sk:] = 1.0
+        m = m.to(dt)
+        case = dict(i=i, b=b, h=h, hk=hk, sq=sq, sk=sk, d=d, dtype=str(dt), kind=kind, er=er, ec=ec,
+                    splits=splits, variant=repr(var))
+        out = mha_fwd_with_mask(q, k, v, m, num_splits=splits, variant=var)
+        assert_close(out, ref_attn_torch(q, k, v, m), str(case))
+        dead = torch.isinf(m[:, :, :sq, :sk].float()).all(-1).squeeze(1)   # [b, sq]
+        if dead.any():
+            assert torch.all(out.permute(0, 2, 1, 3)[dead] == 0), str(case)
+
+
 @pytest.mark.parametrize("shape", [(1, 16, 128, 32768, 128), (4, 16, 2048, 2048, 128),
                                    (2, 16, 1000, 4099, 128), (1, 4, 64, 777, 64)])
 def test_num_splits_for_matches_library_plan(gpu, shape):
