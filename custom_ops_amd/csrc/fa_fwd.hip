@@ -2392,14 +2392,14 @@ static Plan make_plan(const mi355_fa_params* p, int cus, bool allow_stage = true
     pl.map_bytes = pl.live_map ? (size_t)pl.map_full_off + (((size_t)p->b * pl.map_slices + 255) & ~(size_t)255)
                                : 0;
     pl.stage_rs = ceil_div(p->seqlen_k, 8) * 8;
-    // Staged by default except for 8-wave split launches, which run the
-    // compiled kernel either way: there the copy's writes cost what the LDS
-    // DMA saves (cfg5 44.9 staged against 44.7 µs in place, same session),
-    // while unsplit launches reach the assembly loops ([4,16,16,2048,2047]
-    // random mask 150 against 178 µs, top-left causal 139 against 157).
+    // Staged, the mask reaches the assembly loops and the LDS-DMA path of the
+    // compiled kernel, which outrun the register path by more than the copy
+    // costs: [4,16,16,2048,2047] random mask 150 against 178 µs, top-left
+    // causal 139 against 157; cfg5's shape (8 waves, 2 splits, the ping-pong
+    // loop with the map) window 44.2 against 46.5, 10 % random 85.3 against
+    // 93.4 (same sessions, hot).
     pl.staged = !mask_direct && allow_stage && v.stage >= 0 && p->seqlen_k >= 8 &&
-                (uint64_t)p->seqlen_q * pl.stage_rs * 2 < (1ull << 31) &&
-                (v.stage > 0 || !(pl.splits > 1 && pl.waves == 8));
+                (uint64_t)p->seqlen_q * pl.stage_rs * 2 < (1ull << 31);
     pl.stage_bytes = pl.staged ? (((size_t)p->b * p->seqlen_q * pl.stage_rs * 2 + 255) & ~(size_t)255) : 0;
   }
   pl.ws_bytes = pl.o_part_bytes + pl.lse_bytes + pl.ticket_bytes + pl.map_bytes + pl.stage_bytes;
@@ -2511,11 +2511,7 @@ template <int D, bool BF16>
 static bool runs_asm_loop(const KParams& kp, const Plan& pl) {
   // bf16 adds the mask on the matrix core, which needs bf16(1/scale) > 1.0078
   // (-max_bf16 · (1/scale) must overflow to -inf): scale < 0.99
-  // A staged mask's split launches run the compiled kernel, which reads the
-  // live ranges from the map (the loops would scan the staged copy per
-  // workgroup: cfg5's window 57.8 µs against 44.2 hot).
-  return D == 128 && pl.waves == 8 && kp.mask_direct && pl.loop && (!BF16 || kp.scale < 0.99f) &&
-         !(pl.staged && pl.live_map && pl.splits > 1);
+  return D == 128 && pl.waves == 8 && kp.mask_direct && pl.loop && (!BF16 || kp.scale < 0.99f);
 }
 
 template <int D, bool BF16, bool SPLIT>

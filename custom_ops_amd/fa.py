@@ -14,7 +14,7 @@ Mirrors the reference's torch op (Defyli/custom_ops):
 Differences by design: Sk % 8 != 0 pads no K/V (fa_fwd_op.cu:117-134 pads
 K/V/mask); the HIP kernels predicate the key tail in place, and a mask whose
 rows are not 16-byte aligned is staged by a pre-pass into an aligned copy in
-the workspace (all launches but 8-wave split ones). Split-KV partials, the
+the workspace. Split-KV partials, the
 live-tile map and the staged mask come from the caching allocator as one
 workspace tensor sized by the library.
 """

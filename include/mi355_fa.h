@@ -67,9 +67,9 @@ typedef struct mi355_fa_variant {
   int32_t live_map;  /* 0 | 1 always | -1 never: live ranges from the live-tile map
                         pre-pass instead of each workgroup's own scan (default:
                         masks with unaligned rows, and 8-wave split launches)      */
-  int32_t stage;     /* 0 | 1 always | -1 never: masks with unaligned rows are read
-                        from an aligned staged copy in the workspace (default: all
-                        launches but 8-wave split ones) instead of in place        */
+  int32_t stage;     /* 0 | -1: masks with unaligned rows are read in place
+                        (through registers) instead of from an aligned staged
+                        copy in the workspace (1: staged, the default)             */
 } mi355_fa_variant;
 
 /*

@@ -100,7 +100,7 @@ def test_live_range_parity(gpu, loop):
     from custom_ops_amd import Variant, mha_fwd_with_mask
     on, off = Variant(loop=loop, live=1), Variant(loop=loop, live=-1)
     scan = Variant(loop=loop, live=1, live_map=-1)   # unaligned rows: the scan instead of the map
-    # unaligned rows: the staged copy always / never (default: all but 8-wave split launches)
+    # unaligned rows: the staged copy (the default) / the mask read in place
     staged, inplace = Variant(loop=loop, live=1, stage=1), Variant(loop=loop, live=1, stage=-1)
     for n, (kind, b, h, hk, sq, sk, d, dt, splits, xc, xr) in enumerate(CASES):
         g = torch.Generator().manual_seed(1000 + n)
