@@ -123,6 +123,29 @@ def test_cost_model_and_workspace(lib):
 
 
 
+def test_workspace_of_masks_with_unaligned_rows(lib):
+    """The workspace of a mask whose rows are not 16-byte aligned: the
+    live-tile map ([B][ceil(Sq/16)][ceil(tiles/8)] bytes) and its whole-axis
+    flags ([B][ceil(Sq/16)]), then the staged copy ([B][Sq][ceil8(Sk)] 16-bit
+    entries), each rounded up to 256 bytes; Variant(stage=-1) drops the copy,
+    Variant(live_map=-1) the map; an aligned unsplit launch needs none."""
+    from custom_ops_amd import _lib
+    r256 = lambda x: (x + 255) & ~255   # noqa: E731
+    for b, sq, sk in [(1, 128, 259), (2, 1000, 4099), (3, 17, 777)]:
+        common = dict(b=b, seqlen_q=sq, mask_seqlen_q=sq, seqlen_k=sk, mask_seqlen_k=sk,
+                      mask_row_stride=sk, num_splits=1)
+        slices, groups, skp = -(-sq // 16), -(-(-(-sk // 64)) // 8), -(-sk // 8) * 8
+        map_bytes = r256(b * slices * groups) + r256(b * slices)
+        staged = r256(b * sq * skp * 2)
+        assert _lib.workspace_bytes(_params(**common)) == map_bytes + staged, (b, sq, sk)
+        v = _lib.Variant(stage=-1)
+        assert _lib.workspace_bytes(_params(variant=ctypes.pointer(v), **common)) == map_bytes
+        v2 = _lib.Variant(live_map=-1)
+        assert _lib.workspace_bytes(_params(variant=ctypes.pointer(v2), **common)) == staged
+    aligned = dict(seqlen_k=264, mask_seqlen_k=264, mask_row_stride=264, num_splits=1)
+    assert _lib.workspace_bytes(_params(**aligned)) == 0
+
+
 @pytest.mark.parametrize("b,h,sq,sk,d,splits", [
     # configurations of the benchmark (all agree with the measured best)
     (4, 16, 2048, 2048, 128, 1),      # cfg2: 512 workgroups of 8 waves, two rounds
