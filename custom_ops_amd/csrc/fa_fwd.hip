@@ -2054,39 +2054,42 @@ __global__ __launch_bounds__(kCombineThreads) void fa_combine_kernel(const CPara
   const int64_t row0 = (int64_t)blockIdx.x * kRows;
   const int64_t slab = p.rows;
   const int S = p.num_splits;
-  if (S <= 4 && p.part_bytes) {
+  // up to 16 splits in the one-wave form, 4 in the 256-thread one
+  constexpr int kOnePass = kCombineThreads == 64 ? 16 : 4;
+  if (S <= kOnePass && p.part_bytes) {
     // Few splits: each thread loads its row's LSEs and its partial slices
     // together (one round trip instead of the LSE phase's and then the
     // partials') and weighs them itself, no LDS or barrier; the same
     // arithmetic in the same order (bit-identical). cfg5 (2 splits, combine
-    // launch after the ping-pong loop): 44.5 -> 43.1 µs hot.
+    // launch after the ping-pong loop): 44.5 -> 43.1 µs hot; cfg4 (16
+    // splits, one-wave workgroups): 1-2 µs faster.
     const int r = tid / kTPR, c8 = tid % kTPR;
     const int64_t row = row0 + r;
     if (row >= p.rows) return;
     const rsrc_t rp = make_rsrc(p.o_part, p.part_bytes);
     const uint32_t off0 = (uint32_t)((row * D + c8 * 8) * 2);
     const uint32_t sstep = (uint32_t)(slab * D * 2);
-    float l[4];
-    u32x4 raw[4];
+    float l[kOnePass];
+    u32x4 raw[kOnePass];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {   // past S: lse -inf (weight 0), an out-of-range load (0)
+    for (int u = 0; u < kOnePass; ++u) {   // past S: lse -inf (weight 0), an out-of-range load (0)
       l[u] = u < S ? p.lse_part[u * slab + row] : -INFINITY;
       raw[u] = bload16(rp, u < S ? off0 + (uint32_t)u * sstep : 0x80000000u);
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) mx = fmaxf(mx, l[u]);
+    for (int u = 0; u < kOnePass; ++u) mx = fmaxf(mx, l[u]);
     const float mxc = (mx == -INFINITY) ? 0.f : mx;
-    float w[4], sum = 0.f;
+    float w[kOnePass], sum = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kOnePass; ++u) {
       w[u] = __builtin_amdgcn_exp2f((l[u] - mxc) * kLog2e);
       sum += w[u];
     }
     const float inv = (sum > 0.f) ? 1.f / sum : 0.f;
     f32x8 acc = {};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc += (w[u] * inv) * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
+    for (int u = 0; u < kOnePass; ++u) acc += (w[u] * inv) * __builtin_convertvector(bitcast<V8>(raw[u]), f32x8);
     const int64_t bh = row / p.sq;
     const int m = (int)(row % p.sq);
     const int b = (int)(bh / p.h), h = (int)(bh % p.h);
